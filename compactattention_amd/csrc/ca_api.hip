@@ -1,0 +1,326 @@
+// C-ABI entry points of libcompactattn_hip.so: host-side argument validation, then the
+// kernel launches on the caller's stream.  No device allocation, no host synchronisation.
+// Declarations and reference citations are in include/compactattn.h.
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/compactattn.h"
+#include "ca_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok() {
+    g_last_error.clear();
+    return CA_OK;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(CA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
+
+// Validates dims + past blocks and fills the internal shape.
+int check_dims(const ca_dims* d, const int32_t* past_host, ca::Shape* s, ca::PastBlocks* pb,
+               int* max_nkb) {
+    if (d == nullptr) return fail(CA_ERR_INVALID, "dims is NULL");
+    if (past_host == nullptr) return fail(CA_ERR_INVALID, "past_blocks_host is NULL");
+    if (d->batch < 1 || d->batch > CA_MAX_BATCH)
+        return fail(d->batch < 1 ? CA_ERR_INVALID : CA_ERR_LIMIT, "batch=%d outside [1, %d]",
+                    d->batch, CA_MAX_BATCH);
+    if (d->q_len <= 0 || d->q_len % CA_BLOCK != 0)
+        return fail(CA_ERR_INVALID, "q_len=%d must be a positive multiple of %d", d->q_len, CA_BLOCK);
+    if (d->num_q_heads <= 0 || d->num_kv_heads <= 0 || d->num_q_heads % d->num_kv_heads != 0)
+        return fail(CA_ERR_INVALID, "num_q_heads=%d must be a positive multiple of num_kv_heads=%d",
+                    d->num_q_heads, d->num_kv_heads);
+    const int G = d->num_q_heads / d->num_kv_heads;
+    if (G > 16) return fail(CA_ERR_LIMIT, "GQA group size %d > 16", G);
+    const int Qb = d->q_len / CA_BLOCK;
+    int mx = 0;
+    for (int b = 0; b < d->batch; ++b) {
+        if (past_host[b] < 0) return fail(CA_ERR_INVALID, "past_blocks[%d]=%d < 0", b, past_host[b]);
+        if ((int64_t)past_host[b] + Qb > d->kv_cap)
+            return fail(CA_ERR_INVALID, "past_blocks[%d]=%d + q_len/64=%d exceeds kv_cap=%d", b,
+                        past_host[b], Qb, d->kv_cap);
+        pb->p[b] = past_host[b];
+        if (past_host[b] + Qb > mx) mx = past_host[b] + Qb;
+    }
+    for (int b = d->batch; b < CA_MAX_BATCH; ++b) pb->p[b] = 0;
+    if ((int64_t)d->kv_cap * CA_BLOCK > (int64_t)1 << 30)
+        return fail(CA_ERR_LIMIT, "kv_cap=%d blocks too large", d->kv_cap);
+    s->B = d->batch;
+    s->Lq = d->q_len;
+    s->Hq = d->num_q_heads;
+    s->Hkv = d->num_kv_heads;
+    s->G = G;
+    s->Qb = Qb;
+    s->cap = d->kv_cap;
+    s->words = (d->kv_cap + 31) / 32;
+    *max_nkb = mx;
+    return CA_OK;
+}
+
+int check_seq(const ca_seq_layout* l, const char* name, ca::SeqAddr* out) {
+    if (l == nullptr || l->data == nullptr) return fail(CA_ERR_INVALID, "%s is NULL", name);
+    if (!aligned16(l->data)) return fail(CA_ERR_INVALID, "%s data must be 16-byte aligned", name);
+    if (l->stride_b % 8 || l->stride_t % 8 || l->stride_h % 8 || l->stride_t <= 0 || l->stride_h <= 0 ||
+        l->stride_b < 0)
+        return fail(CA_ERR_INVALID, "%s strides (b=%lld, t=%lld, h=%lld) must be multiples of 8 and t,h > 0",
+                    name, (long long)l->stride_b, (long long)l->stride_t, (long long)l->stride_h);
+    out->data = static_cast<uint16_t*>(l->data);
+    out->sb = l->stride_b;
+    out->st = l->stride_t;
+    out->sh = l->stride_h;
+    return CA_OK;
+}
+
+int check_kv(const ca_kv_layout* l, const char* name, int max_nkb, ca::KvAddr* out) {
+    if (l == nullptr || l->data == nullptr) return fail(CA_ERR_INVALID, "%s is NULL", name);
+    if (!aligned16(l->data)) return fail(CA_ERR_INVALID, "%s data must be 16-byte aligned", name);
+    if (l->stride_b % 8 || l->stride_h % 8 || l->stride_blk % 8 || l->stride_tok % 8 || l->stride_tok <= 0 ||
+        l->stride_b < 0 || l->stride_h < 0 || l->stride_blk < 0)
+        return fail(CA_ERR_INVALID, "%s strides must be non-negative multiples of 8 (stride_tok > 0)", name);
+    if (l->page_table != nullptr) {
+        if (!aligned4(l->page_table)) return fail(CA_ERR_INVALID, "%s page_table misaligned", name);
+        if (l->page_table_stride < max_nkb)
+            return fail(CA_ERR_INVALID, "%s page_table_stride=%lld < blocks per row %d", name,
+                        (long long)l->page_table_stride, max_nkb);
+    }
+    out->data = static_cast<uint16_t*>(l->data);
+    out->sb = l->stride_b;
+    out->sh = l->stride_h;
+    out->sblk = l->stride_blk;
+    out->stok = l->stride_tok;
+    out->page_table = l->page_table;
+    out->pts = l->page_table_stride;
+    return CA_OK;
+}
+
+int check_rope(const float* c, const float* s, int64_t rows, int max_nkb) {
+    if ((c == nullptr) != (s == nullptr)) return fail(CA_ERR_INVALID, "rope_cos and rope_sin must both be set or both NULL");
+    if (c != nullptr && rows < max_nkb)
+        return fail(CA_ERR_INVALID, "rope_rows=%lld < highest block id + 1 = %d", (long long)rows, max_nkb);
+    if (c != nullptr && (!aligned4(c) || !aligned4(s))) return fail(CA_ERR_INVALID, "rope tables misaligned");
+    return CA_OK;
+}
+
+int check_rule(const ca_select_rule* r) {
+    if (r == nullptr) return fail(CA_ERR_INVALID, "rule is NULL");
+    if (r->flags & ~(CA_RULE_TOPK | CA_RULE_ALPHA | CA_RULE_THRESHOLD))
+        return fail(CA_ERR_INVALID, "unknown rule flags 0x%x", r->flags);
+    if ((r->flags & CA_RULE_TOPK) && r->topk < 0) return fail(CA_ERR_INVALID, "topk=%d < 0", r->topk);
+    return CA_OK;
+}
+
+constexpr size_t kMaxLds = 160 * 1024 - 4096;  // dynamic LDS budget next to static arrays
+
+}  // namespace
+
+extern "C" {
+
+int ca_abi_version(void) { return CA_ABI_VERSION; }
+
+const char* ca_last_error(void) { return g_last_error.c_str(); }
+
+int ca_cache_fill(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_layout* v_new,
+                  const ca_kv_layout* k_cache, const ca_kv_layout* v_cache,
+                  const int32_t* past_blocks_host, float* kmean, const float* gate_wk,
+                  const float* rope_cos, const float* rope_sin, int64_t rope_rows, float* kgate,
+                  void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    ca::SeqAddr kn, vn;
+    ca::KvAddr kc, vc;
+    if ((rc = check_seq(k_new, "k_new", &kn)) != CA_OK) return rc;
+    if ((rc = check_seq(v_new, "v_new", &vn)) != CA_OK) return rc;
+    if ((rc = check_kv(k_cache, "k_cache", max_nkb, &kc)) != CA_OK) return rc;
+    if ((rc = check_kv(v_cache, "v_cache", max_nkb, &vc)) != CA_OK) return rc;
+    if (kmean != nullptr && !aligned16(kmean)) return fail(CA_ERR_INVALID, "kmean misaligned");
+    if (gate_wk != nullptr) {
+        if (kgate == nullptr) return fail(CA_ERR_INVALID, "gate_wk given without kgate");
+        if ((rc = check_rope(rope_cos, rope_sin, rope_rows, max_nkb)) != CA_OK) return rc;
+    }
+    hipError_t e = ca::launch_cache_fill(s, kn, vn, kc, vc, pb, kmean, gate_wk, rope_cos, rope_sin,
+                                         kgate, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "cache_fill launch");
+    return ok();
+}
+
+int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* past_blocks_host,
+                  const float* gate_wq, const float* rope_cos, const float* rope_sin,
+                  int64_t rope_rows, float* qhat, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    ca::SeqAddr qa;
+    if ((rc = check_seq(q, "q", &qa)) != CA_OK) return rc;
+    if (qhat == nullptr) return fail(CA_ERR_INVALID, "qhat is NULL");
+    if (gate_wq != nullptr && (rc = check_rope(rope_cos, rope_sin, rope_rows, max_nkb)) != CA_OK) return rc;
+    hipError_t e = ca::launch_pool_query(s, qa, pb, gate_wq, gate_wq ? rope_cos : nullptr,
+                                         gate_wq ? rope_sin : nullptr, qhat,
+                                         static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "pool_query launch");
+    return ok();
+}
+
+int ca_score_select(const ca_dims* dims, const float* qhat, const float* khat, float scale,
+                    const ca_select_rule* rule, const int32_t* past_blocks_host, uint32_t* rowmask,
+                    float* scores_out, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    if ((rc = check_rule(rule)) != CA_OK) return rc;
+    if (qhat == nullptr || khat == nullptr || rowmask == nullptr)
+        return fail(CA_ERR_INVALID, "qhat, khat and rowmask are required");
+    if (!aligned16(khat)) return fail(CA_ERR_INVALID, "khat must be 16-byte aligned");
+    if (ca::score_select_lds_bytes(s, true) > kMaxLds)
+        return fail(CA_ERR_LIMIT, "group %d x kv_cap %d scores do not fit in LDS", s.G, s.cap);
+    hipError_t e = ca::launch_score_select(s, qhat, khat, scale, nullptr, 0, 0, 0, 0, *rule, pb, rowmask,
+                                           scores_out, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "score_select launch");
+    return ok();
+}
+
+int ca_select_scores(const ca_dims* dims, const void* scores, int32_t dtype, int64_t stride_b,
+                     int64_t stride_h, int64_t stride_q, const ca_select_rule* rule,
+                     const int32_t* past_blocks_host, uint32_t* rowmask, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    if ((rc = check_rule(rule)) != CA_OK) return rc;
+    if (scores == nullptr || rowmask == nullptr) return fail(CA_ERR_INVALID, "scores and rowmask are required");
+    if (dtype != 0 && dtype != 1) return fail(CA_ERR_INVALID, "dtype=%d (0 = fp32, 1 = bf16)", dtype);
+    if (stride_b < 0 || stride_h < 0 || stride_q < 0) return fail(CA_ERR_INVALID, "negative score stride");
+    if (ca::score_select_lds_bytes(s, false) > kMaxLds)
+        return fail(CA_ERR_LIMIT, "group %d x kv_cap %d scores do not fit in LDS", s.G, s.cap);
+    hipError_t e = ca::launch_score_select(s, nullptr, nullptr, 0.0f, scores, dtype, stride_b, stride_h,
+                                           stride_q, *rule, pb, rowmask, nullptr,
+                                           static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "select_scores launch");
+    return ok();
+}
+
+int ca_union_compact(const ca_dims* dims, const uint32_t* rowmask, int32_t last_n_block,
+                     const int32_t* past_blocks_host, uint8_t* keep_block, uint8_t* keep_kv,
+                     int32_t* table, int64_t table_stride, int32_t* counts, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    if (rowmask == nullptr || table == nullptr || counts == nullptr)
+        return fail(CA_ERR_INVALID, "rowmask, table and counts are required");
+    if (table_stride < s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, s.cap);
+    if (sizeof(uint32_t) * (size_t)s.words > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
+    hipError_t e = ca::launch_union_compact(s, rowmask, last_n_block, nullptr, pb, keep_block, keep_kv, table,
+                                            table_stride, counts, false, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "union_compact launch");
+    return ok();
+}
+
+int ca_compact_keep_kv(const ca_dims* dims, const uint8_t* keep_kv, const int32_t* past_blocks_host,
+                       int32_t* table, int64_t table_stride, int32_t* counts, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    if (keep_kv == nullptr || table == nullptr || counts == nullptr)
+        return fail(CA_ERR_INVALID, "keep_kv, table and counts are required");
+    if (table_stride < s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, s.cap);
+    if (sizeof(uint32_t) * (size_t)s.words > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
+    hipError_t e = ca::launch_union_compact(s, nullptr, 0, keep_kv, pb, nullptr, nullptr, table, table_stride,
+                                            counts, false, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "compact_keep_kv launch");
+    return ok();
+}
+
+int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t* table,
+                   int64_t table_stride, int32_t* counts, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    if (table == nullptr || counts == nullptr) return fail(CA_ERR_INVALID, "table and counts are required");
+    if (table_stride < s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, s.cap);
+    if (sizeof(uint32_t) * (size_t)s.words > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
+    hipError_t e = ca::launch_union_compact(s, nullptr, 0, nullptr, pb, nullptr, nullptr, table, table_stride,
+                                            counts, true, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "dense_table launch");
+    return ok();
+}
+
+int32_t ca_attn_pick_splits(const ca_dims* dims, const int32_t* past_blocks_host) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0;
+    if (check_dims(dims, past_blocks_host, &s, &pb, &max_nkb) != CA_OK) return -1;
+    return ca::attn_pick_splits(s, pb);
+}
+
+int64_t ca_attn_workspace_size(const ca_dims* dims, const int32_t* past_blocks_host, int32_t num_splits) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0;
+    if (check_dims(dims, past_blocks_host, &s, &pb, &max_nkb) != CA_OK) return -1;
+    if (num_splits == 0) num_splits = ca::attn_pick_splits(s, pb);
+    if (num_splits < 1 || num_splits > 16) return fail(CA_ERR_INVALID, "num_splits=%d outside [1, 16]", num_splits);
+    return ca::attn_workspace_bytes(s, num_splits);
+}
+
+int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout* k,
+                const ca_kv_layout* v, const int32_t* table, int64_t table_stride,
+                const int32_t* counts, const int32_t* past_blocks_host, float scale,
+                const ca_seq_layout* out, float* lse, int32_t num_splits, void* workspace,
+                int64_t workspace_bytes, void* stream) {
+    ca::AttnArgs a;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &a.s, &a.pb, &max_nkb)) != CA_OK) return rc;
+    if ((rc = check_seq(q, "q", &a.q)) != CA_OK) return rc;
+    if ((rc = check_seq(out, "out", &a.out)) != CA_OK) return rc;
+    if ((rc = check_kv(k, "k", max_nkb, &a.k)) != CA_OK) return rc;
+    if ((rc = check_kv(v, "v", max_nkb, &a.v)) != CA_OK) return rc;
+    if (table == nullptr || counts == nullptr) return fail(CA_ERR_INVALID, "table and counts are required");
+    if (table_stride < a.s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, a.s.cap);
+    if (!(scale > 0.0f)) return fail(CA_ERR_INVALID, "scale must be positive");
+    if ((int64_t)a.s.Lq * a.s.G > (int64_t)1 << 24) return fail(CA_ERR_LIMIT, "q_len * group too large");
+    if (num_splits == 0) num_splits = ca::attn_pick_splits(a.s, a.pb);
+    if (num_splits < 1 || num_splits > 16) return fail(CA_ERR_INVALID, "num_splits=%d outside [1, 16]", num_splits);
+    const int64_t need = ca::attn_workspace_bytes(a.s, num_splits);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+        return fail(CA_ERR_WORKSPACE, "num_splits=%d needs a 16-byte aligned workspace of %lld bytes (got %lld)",
+                    num_splits, (long long)need, (long long)workspace_bytes);
+    a.table = table;
+    a.table_stride = table_stride;
+    a.counts = counts;
+    a.scale = scale;
+    a.lse = lse;
+    a.num_splits = num_splits;
+    a.workspace = workspace;
+    hipError_t e = ca::launch_attn(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "attn launch");
+    return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,453 @@
+// Indexed attention prefill over selected KV blocks: bf16 MFMA (gfx950
+// v_mfma_f32_32x32x16_bf16), online softmax, K/V blocks read through the block table.
+//
+// Reference semantics: flash_attn_with_kvcache / FlashInfer paged prefill as driven by
+// compact_attn/kernels/varlen/indexed_dense_prefill_varlen.py:1473-1613 and
+// compact_attn/kernels/varlen/flashinfer_zero_copy_prefill.py:1139-1353 (GQA-packed rows,
+// bottom-right causal), restated without a gather in
+// compact_attn/kernels/varlen/indexed_dense_prefill_direct_triton.py:91-241.
+//
+// Work decomposition
+//  - The G query heads of a KV group share the group's block table, so a KV row
+//    (request, kv head) owns Lq*G "packed" query rows r = t*G + g (token t, head g).
+//  - A workgroup (4 waves) takes 256 packed rows; each wave keeps 64 rows (two 32-row MFMA
+//    tiles) for the whole KV loop: Q in VGPRs, O^T in accumulators.
+//  - Scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q from VGPRs), so the
+//    softmax output lands in exactly the VGPR layout the second product's B operand needs:
+//    O^T += V^T P^T (A = V^T from LDS).  Inside each 32-key S^T tile the A-row -> key map
+//    swaps bits 2 and 3 of the row index, which makes every lane's 8 P values 8 consecutive
+//    keys, i.e. one 16-byte V^T read.
+//  - K blocks are stored in LDS row-major with a 16-byte-chunk XOR swizzle; V blocks are
+//    transposed on their way into LDS (register 8x4 transpose) so V^T rows are contiguous.
+//  - Two LDS stages: the next block's global loads are in flight while the current block is
+//    computed.  Optional split of each row's block list (split-KV) with an LSE merge.
+//  - Workgroup ids are remapped so consecutive work items (same KV row) share an XCD and
+//    its L2.
+
+#include "ca_common.h"
+#include "ca_kernels.h"
+
+namespace ca {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kBM = 256;             // packed query rows per workgroup
+constexpr int kKvBytes = 64 * 128 * 2;  // one 64-token K or V block in bf16
+constexpr float kRescale = 8.0f;      // lazy-rescale slack (log2 units)
+
+struct AttnParams {
+    Shape s;
+    SeqAddr q;
+    KvAddr k, v;
+    const int32_t* table;
+    int64_t table_stride;
+    const int32_t* counts;
+    PastBlocks pb;
+    float scale_log2;  // softmax scale * log2(e)
+    SeqAddr out;
+    float* lse;
+    int splits;
+    int ntiles;       // packed-row tiles per KV row
+    int rows_total;   // Lq * G
+    int total_items;  // B*Hkv*ntiles*splits
+    int per_xcd;      // ceil(total_items / 8)
+    float* ws_o;      // [splits][B*Hkv][rows_total][128]
+    float* ws_lse;    // [splits][B*Hkv][rows_total]  (log2 domain)
+};
+
+__device__ __forceinline__ int swap23(int m) {
+    return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1);
+}
+
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
+    return (a & 0xffffu) | (b << 16);
+}
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
+    return (a >> 16) | (b & 0xffff0000u);
+}
+
+
+__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][kKvBytes];  // [stage][K, V^T]
+
+    const int L = blockIdx.x;
+    const int W = (L & 7) * p.per_xcd + (L >> 3);
+    if (W >= p.total_items) return;
+    const Shape& s = p.s;
+    const int split = W % p.splits;
+    const int tmp = W / p.splits;
+    const int tile = tmp % p.ntiles;
+    const int row = tmp / p.ntiles;
+    const int b = row / s.Hkv;
+    const int hk = row - b * s.Hkv;
+    const int G = s.G;
+    const int P = p.pb.p[b];
+    const int rows_total = p.rows_total;
+    const int r0 = tile * kBM;
+    const int t_first = r0 / G;
+    const int t_last = min(r0 + kBM - 1, rows_total - 1) / G;
+
+    const int32_t* tab = p.table + (int64_t)row * p.table_stride;
+    const int nkb = P + s.Qb;  // valid logical block ids are [0, nkb)
+    const int cnt = min(max(p.counts[row], 0), s.cap);
+    const int lim = P + t_last / 64;
+    int n_vis = cnt;
+    while (n_vis > 0 && tab[n_vis - 1] > lim) --n_vis;
+    const int chunk = (n_vis + p.splits - 1) / p.splits;
+    const int e0 = min(n_vis, split * chunk);
+    const int e1 = min(n_vis, e0 + chunk);
+
+    const int tid = threadIdx.x;
+    const int w = tid >> 6;
+    const int l = tid & 63;
+    const int h = l >> 5;
+    const int n = l & 31;
+
+    // ---- Q fragments (B operand of S^T = K Q^T) ----
+    bf16x8_t qf[2][8];
+    int qtok[2];
+    int qg[2];
+    bool qvalid[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const int r = r0 + 64 * w + 32 * rt + n;
+        qvalid[rt] = r < rows_total;
+        const int t = qvalid[rt] ? r / G : 0;
+        const int g = qvalid[rt] ? r - t * G : 0;
+        qtok[rt] = qvalid[rt] ? t : 0x3fffffff;
+        qg[rt] = g;
+        const uint16_t* qp = p.q.data + b * p.q.sb + (int64_t)t * p.q.st + (int64_t)(hk * G + g) * p.q.sh + 8 * h;
+#pragma unroll
+        for (int ds = 0; ds < 8; ++ds) {
+            if (qvalid[rt]) {
+                qf[rt][ds] = *reinterpret_cast<const bf16x8_t*>(qp + 16 * ds);
+            } else {
+                u32x4_t z = {0u, 0u, 0u, 0u};
+                qf[rt][ds] = __builtin_bit_cast(bf16x8_t, z);
+            }
+        }
+    }
+
+    f32x16_t oacc[4][2];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) oacc[dt][rt][j] = 0.0f;
+    float m_run[2] = {-__builtin_inff(), -__builtin_inff()};
+    float l_run[2] = {0.0f, 0.0f};
+
+    const uint16_t* kbase_row = p.k.data + b * p.k.sb + hk * p.k.sh;
+    const uint16_t* vbase_row = p.v.data + b * p.v.sb + hk * p.v.sh;
+    const int32_t* kpt = p.k.page_table ? p.k.page_table + (int64_t)row * p.k.pts : nullptr;
+    const int32_t* vpt = p.v.page_table ? p.v.page_table + (int64_t)row * p.v.pts : nullptr;
+
+    // per-thread global->LDS assignment; 32-bit element offsets inside one 64-token block
+    // (the host checks 64 * stride_tok < 2^30) on top of a wave-uniform block base
+    const int k_key0 = tid >> 4;      // + 16*i
+    const int k_chunk = tid & 15;
+    const int v_kg = tid >> 5;        // keys 8*v_kg .. +7
+    const int v_dg = tid & 31;        // d 4*v_dg .. +3
+    const uint32_t kstok = static_cast<uint32_t>(p.k.stok);
+    const uint32_t vstok = static_cast<uint32_t>(p.v.stok);
+    const uint32_t k_off0 = static_cast<uint32_t>(k_key0) * kstok + 8u * k_chunk;
+    const uint32_t v_off0 = static_cast<uint32_t>(8 * v_kg) * vstok + 4u * v_dg;
+
+    u32x4_t kreg[4];
+    u32x2_t vreg[8];
+
+    // table entries are clamped into [0, nkb) so a corrupt table cannot address outside
+    // the KV tensors
+    auto block_id = [&](int e) { return min(max(tab[e], 0), nkb - 1); };
+    auto load_block = [&](int e) {
+        const int kb = block_id(e);
+        const int64_t kphys = kpt ? kpt[kb] : kb;
+        const int64_t vphys = vpt ? vpt[kb] : kb;
+        const uint16_t* kb_ptr = kbase_row + kphys * p.k.sblk;
+        const uint16_t* vb_ptr = vbase_row + vphys * p.v.sblk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            kreg[i] = *reinterpret_cast<const u32x4_t*>(kb_ptr + (k_off0 + static_cast<uint32_t>(i) * 16u * kstok));
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+            vreg[r] = *reinterpret_cast<const u32x2_t*>(vb_ptr + (v_off0 + static_cast<uint32_t>(r) * vstok));
+    };
+    auto store_block = [&](int stage) {
+        uint8_t* ks = smem[stage][0];
+        uint8_t* vs = smem[stage][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int key = k_key0 + 16 * i;
+            const int phys = k_chunk ^ (key & 15);
+            *reinterpret_cast<u32x4_t*>(ks + key * 256 + phys * 16) = kreg[i];
+        }
+        // transpose 8 keys x 4 d into 4 rows of V^T (8 keys each)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            u32x4_t o;
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+                const uint32_t a = (j < 2) ? vreg[2 * q2].x : vreg[2 * q2].y;
+                const uint32_t c = (j < 2) ? vreg[2 * q2 + 1].x : vreg[2 * q2 + 1].y;
+                o[q2] = (j & 1) ? pack_hi(a, c) : pack_lo(a, c);
+            }
+            const int d = 4 * v_dg + j;
+            const int phys = v_kg ^ ((d >> 1) & 7);
+            *reinterpret_cast<u32x4_t*>(vs + d * 128 + phys * 16) = o;
+        }
+    };
+
+    const float sl2 = p.scale_log2;
+
+    if (e0 < e1) {
+        load_block(e0);
+        store_block(0);
+        __syncthreads();
+    }
+    for (int e = e0; e < e1; ++e) {
+        const int stage = (e - e0) & 1;
+        const bool has_next = e + 1 < e1;
+        if (has_next) load_block(e + 1);
+        const int kb = block_id(e);
+        const uint8_t* ks = smem[stage][0];
+        const uint8_t* vs = smem[stage][1];
+
+        // The 64-key block is processed as two 32-key halves, each one online-softmax step:
+        // S^T_half (32 keys x 64 rows) -> P -> O^T += V^T_half P^T_half.
+        const bool need_mask = kb * 64 + 63 > P * 64 + t_first;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+            // ---- S^T = K Q^T for keys kt*32 .. kt*32+31 ----
+            f32x16_t sacc[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) sacc[rt][j] = 0.0f;
+            const int kk = kt * 32 + swap23(n);
+#pragma unroll
+            for (int ds = 0; ds < 8; ++ds) {
+                const int phys = (2 * ds + h) ^ (kk & 15);
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + kk * 256 + phys * 16);
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+                    sacc[rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[rt][ds], sacc[rt], 0, 0, 0);
+            }
+
+            // ---- online softmax (log2 domain, lazy rescale) ----
+            // m_run is only raised when a row's max exceeds it by more than kRescale (log2
+            // units); otherwise P = exp2(s - m_run) < 2^kRescale and O^T / l keep their scale,
+            // so the accumulators are rarely touched by VALU code.
+            float alpha[2];
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) {
+                // key kt*32 + swap23(8*(j/4) + 4*h + j%4) = kt*32 + 8*h + key_off(j) is visible
+                // iff its position kb*64 + key <= 64*P + t
+                const int vis = P * 64 + qtok[rt] - kb * 64 - kt * 32 - 8 * h;
+                float mx = -__builtin_inff();
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    float v = sacc[rt][j] * sl2;
+                    const int key_off = 16 * (j >> 3) + 4 * ((j >> 2) & 1) + (j & 3);
+                    if (need_mask && key_off > vis) v = -__builtin_inff();
+                    sacc[rt][j] = v;
+                    mx = fmaxf(mx, v);
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                alpha[rt] = 1.0f;
+                if (mx > m_run[rt] + kRescale) {
+                    alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - mx);  // 0 when m_run = -inf
+                    m_run[rt] = mx;
+                }
+                const float m_use = m_run[rt] == -__builtin_inff() ? 0.0f : m_run[rt];
+                float rs = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const float pv = __builtin_amdgcn_exp2f(sacc[rt][j] - m_use);
+                    sacc[rt][j] = pv;
+                    rs += pv;
+                }
+                rs += __shfl_xor(rs, 32, 64);
+                l_run[rt] = l_run[rt] * alpha[rt] + rs;
+            }
+            if (__ballot(alpha[0] != 1.0f || alpha[1] != 1.0f)) {
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                        for (int j = 0; j < 16; ++j) oacc[dt][rt][j] *= alpha[rt];
+            }
+
+            // ---- O^T += V^T P^T over the same 32 keys ----
+#pragma unroll
+            for (int sh = 0; sh < 2; ++sh) {
+                const int s4 = 2 * kt + sh;
+                bf16x8_t pf[2];
+#pragma unroll
+                for (int rt = 0; rt < 2; ++rt) {
+                    f32x8_t pv8;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) pv8[i] = sacc[rt][8 * sh + i];
+                    pf[rt] = __builtin_convertvector(pv8, bf16x8_t);
+                }
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const int d = dt * 32 + n;
+                    const int phys = (2 * s4 + h) ^ ((d >> 1) & 7);
+                    const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(vs + d * 128 + phys * 16);
+#pragma unroll
+                    for (int rt = 0; rt < 2; ++rt)
+                        oacc[dt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[rt], oacc[dt][rt], 0, 0, 0);
+                }
+            }
+        }
+
+        if (has_next) store_block(stage ^ 1);
+        __syncthreads();
+    }
+
+    // ---- epilogue ----
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        if (!qvalid[rt]) continue;
+        const int r = r0 + 64 * w + 32 * rt + n;
+        const float lsum = l_run[rt];
+        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+        const float lse2 = lsum > 0.0f ? m_run[rt] + __log2f(lsum) : -__builtin_inff();
+        if (p.splits == 1) {
+            const int t = qtok[rt];
+            const int hq = hk * G + qg[rt];
+            uint16_t* op = p.out.data + b * p.out.sb + (int64_t)t * p.out.st + (int64_t)hq * p.out.sh;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int d0 = dt * 32 + 8 * jq + 4 * h;
+                    f32x4_t o4;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) o4[i] = oacc[dt][rt][4 * jq + i] * inv;
+                    *reinterpret_cast<bf16x4_t*>(op + d0) = __builtin_convertvector(o4, bf16x4_t);
+                }
+            if (p.lse && h == 0) p.lse[((int64_t)b * s.Hq + hq) * s.Lq + t] = lse2 * 0.69314718055994531f;
+        } else {
+            const int64_t prow = ((int64_t)split * (s.B * s.Hkv) + row) * rows_total + r;
+            float* wo = p.ws_o + prow * 128;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int jq = 0; jq < 4; ++jq) {
+                    const int d0 = dt * 32 + 8 * jq + 4 * h;
+                    float4 o;
+                    o.x = oacc[dt][rt][4 * jq + 0] * inv;
+                    o.y = oacc[dt][rt][4 * jq + 1] * inv;
+                    o.z = oacc[dt][rt][4 * jq + 2] * inv;
+                    o.w = oacc[dt][rt][4 * jq + 3] * inv;
+                    *reinterpret_cast<float4*>(wo + d0) = o;
+                }
+            if (h == 0) p.ws_lse[prow] = lse2;
+        }
+    }
+}
+
+// Merge split partials: one packed row per 32 threads, 4 head-dim lanes per thread.
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
+    const Shape& s = p.s;
+    const int64_t gid = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int64_t rows_all = (int64_t)s.B * s.Hkv * p.rows_total;
+    if (gid >= rows_all) return;
+    const int lane = threadIdx.x & 31;
+    const int row = static_cast<int>(gid / p.rows_total);
+    const int r = static_cast<int>(gid - (int64_t)row * p.rows_total);
+    const int b = row / s.Hkv;
+    const int hk = row - b * s.Hkv;
+    const int t = r / s.G;
+    const int g = r - t * s.G;
+    float mx = -__builtin_inff();
+    for (int sp = 0; sp < p.splits; ++sp) mx = fmaxf(mx, p.ws_lse[(int64_t)sp * rows_all + gid]);
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float wsum = 0.0f;
+    if (mx != -__builtin_inff()) {
+        for (int sp = 0; sp < p.splits; ++sp) {
+            const float ls = p.ws_lse[(int64_t)sp * rows_all + gid];
+            const float wgt = __builtin_amdgcn_exp2f(ls - mx);
+            if (wgt == 0.0f) continue;
+            const float4 o = *reinterpret_cast<const float4*>(p.ws_o + ((int64_t)sp * rows_all + gid) * 128 + 4 * lane);
+            acc[0] += wgt * o.x;
+            acc[1] += wgt * o.y;
+            acc[2] += wgt * o.z;
+            acc[3] += wgt * o.w;
+            wsum += wgt;
+        }
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+    const int hq = hk * s.G + g;
+    uint16_t* op = p.out.data + b * p.out.sb + (int64_t)t * p.out.st + (int64_t)hq * p.out.sh + 4 * lane;
+    f32x4_t o4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o4[i] = acc[i] * inv;
+    *reinterpret_cast<bf16x4_t*>(op) = __builtin_convertvector(o4, bf16x4_t);
+    if (p.lse && lane == 0)
+        p.lse[((int64_t)b * s.Hq + hq) * s.Lq + t] =
+            wsum > 0.0f ? (mx + __log2f(wsum)) * 0.69314718055994531f : -__builtin_inff();
+}
+
+}  // namespace
+
+int attn_pick_splits(const Shape& s, const PastBlocks& pb) {
+    const int rows_total = s.Lq * s.G;
+    const int ntiles = (rows_total + kBM - 1) / kBM;
+    const int items = s.B * s.Hkv * ntiles;
+    int max_blocks = 0;
+    for (int b = 0; b < s.B; ++b) max_blocks = max(max_blocks, pb.p[b] + s.Qb);
+    int splits = (256 + items - 1) / items;  // fill the 256 CUs
+    const int by_work = max(1, max_blocks / 32);
+    if (splits > by_work) splits = by_work;
+    if (splits > 16) splits = 16;
+    if (splits < 1) splits = 1;
+    return splits;
+}
+
+int64_t attn_workspace_bytes(const Shape& s, int num_splits) {
+    if (num_splits <= 1) return 0;
+    const int64_t rows_all = (int64_t)s.B * s.Hkv * s.Lq * s.G;
+    return (int64_t)num_splits * rows_all * (128 + 1) * (int64_t)sizeof(float);
+}
+
+hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
+    AttnParams p;
+    p.s = a.s;
+    p.q = a.q;
+    p.k = a.k;
+    p.v = a.v;
+    p.table = a.table;
+    p.table_stride = a.table_stride;
+    p.counts = a.counts;
+    p.pb = a.pb;
+    p.scale_log2 = a.scale * 1.4426950408889634f;
+    p.out = a.out;
+    p.lse = a.lse;
+    p.splits = a.num_splits;
+    p.rows_total = a.s.Lq * a.s.G;
+    p.ntiles = (p.rows_total + kBM - 1) / kBM;
+    p.total_items = a.s.B * a.s.Hkv * p.ntiles * p.splits;
+    p.per_xcd = (p.total_items + 7) / 8;
+    const int64_t rows_all = (int64_t)a.s.B * a.s.Hkv * p.rows_total;
+    p.ws_o = a.num_splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
+    p.ws_lse = a.num_splits > 1 ? p.ws_o + (int64_t)a.num_splits * rows_all * 128 : nullptr;
+    hipLaunchKernelGGL(attn_fwd_kernel, dim3(p.per_xcd * 8), dim3(256), 0, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || a.num_splits <= 1) return e;
+    const int64_t blocks = (rows_all + 7) / 8;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace ca

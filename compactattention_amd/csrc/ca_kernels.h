@@ -1,0 +1,73 @@
+// Internal launch interface between the C-ABI layer (ca_api.cpp) and the kernels.
+// Shapes reaching these launchers have already been validated on the host.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/compactattn.h"
+
+namespace ca {
+
+struct PastBlocks {
+    int32_t p[CA_MAX_BATCH];
+};
+
+struct KvAddr {
+    uint16_t* data;
+    int64_t sb, sh, sblk, stok;
+    const int32_t* page_table;
+    int64_t pts;
+};
+
+struct SeqAddr {
+    uint16_t* data;
+    int64_t sb, st, sh;
+};
+
+struct Shape {
+    int B, Lq, Hq, Hkv, G, Qb, cap, words;
+};
+
+hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr& v_new,
+                             const KvAddr& k_cache, const KvAddr& v_cache, const PastBlocks& pb,
+                             float* kmean, const float* wk, const float* rope_cos,
+                             const float* rope_sin, float* kgate, hipStream_t stream);
+
+hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks& pb, const float* wq,
+                             const float* rope_cos, const float* rope_sin, float* qhat,
+                             hipStream_t stream);
+
+// LDS bytes the score/select kernel needs for this shape (0 if unsupported).
+size_t score_select_lds_bytes(const Shape& s, bool compute);
+
+hipError_t launch_score_select(const Shape& s, const float* qhat, const float* khat, float scale,
+                               const void* scores_in, int dtype, int64_t ssb, int64_t ssh,
+                               int64_t ssq, const ca_select_rule& rule, const PastBlocks& pb,
+                               uint32_t* rowmask, float* scores_out, hipStream_t stream);
+
+hipError_t launch_union_compact(const Shape& s, const uint32_t* rowmask, int last_n_block,
+                                const uint8_t* keep_kv_in, const PastBlocks& pb, uint8_t* keep_block,
+                                uint8_t* keep_kv, int32_t* table, int64_t table_stride,
+                                int32_t* counts, bool dense, hipStream_t stream);
+
+struct AttnArgs {
+    Shape s;
+    SeqAddr q;
+    KvAddr k, v;
+    const int32_t* table;
+    int64_t table_stride;
+    const int32_t* counts;
+    PastBlocks pb;
+    float scale;
+    SeqAddr out;
+    float* lse;
+    int num_splits;
+    void* workspace;
+};
+
+int attn_pick_splits(const Shape& s, const PastBlocks& pb);
+int64_t attn_workspace_bytes(const Shape& s, int num_splits);
+hipError_t launch_attn(const AttnArgs& a, hipStream_t stream);
+
+}  // namespace ca

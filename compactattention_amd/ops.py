@@ -1,0 +1,327 @@
+"""Torch-tensor front end of the C-ABI (one function per entry point).
+
+Each wrapper checks devices/dtypes, builds the layout structs from tensor strides and
+launches on ``torch.cuda.current_stream()``.  Outputs are allocated with torch's caching
+allocator here (the C-ABI itself never allocates).  Nothing in this module falls back to
+a non-HIP implementation.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence, Tuple
+
+import torch
+
+from . import _hip
+from ._hip import BLOCK, HEAD_DIM, Dims, KvLayout, SelectRule, SeqLayout, check
+
+
+@dataclass(frozen=True)
+class Rule:
+    """Block selection rule (``ca_select_rule``).
+
+    topk       keep the top-k past blocks of every (head, query block) row, ordered by
+               (score desc, block id asc) -- the reference's ``min_budget``;
+    alpha      keep blocks with score >= alpha * row max (FlashPrefill);
+    threshold  keep blocks with score > threshold (SeerAttention, strict);
+    sink_blocks / window_blocks / local_blocks / last_n_block as in ``ca_select_rule``.
+    """
+
+    topk: int = 0
+    alpha: Optional[float] = None
+    threshold: Optional[float] = None
+    sink_blocks: int = 0
+    window_blocks: int = 0
+    local_blocks: int = 0
+    last_n_block: int = 0
+
+    def to_c(self) -> SelectRule:
+        flags = 0
+        if self.topk > 0:
+            flags |= _hip.RULE_TOPK
+        if self.alpha is not None:
+            flags |= _hip.RULE_ALPHA
+        if self.threshold is not None:
+            flags |= _hip.RULE_THRESHOLD
+        return SelectRule(
+            flags,
+            int(self.topk),
+            float(self.alpha if self.alpha is not None else 0.0),
+            float(self.threshold if self.threshold is not None else 0.0),
+            int(self.sink_blocks),
+            int(self.window_blocks),
+            int(self.local_blocks),
+            int(self.last_n_block),
+        )
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _need_cuda(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a GPU tensor (got device {t.device})")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
+
+
+def past_array(past_blocks: Sequence[int]):
+    vals = [int(x) for x in past_blocks]
+    if not 1 <= len(vals) <= _hip.MAX_BATCH:
+        raise ValueError(f"batch must be in [1, {_hip.MAX_BATCH}]")
+    return (ctypes.c_int32 * len(vals))(*vals)
+
+
+def make_dims(batch: int, q_len: int, num_q_heads: int, num_kv_heads: int, kv_cap: int) -> Dims:
+    return Dims(int(batch), int(q_len), int(num_q_heads), int(num_kv_heads), int(kv_cap))
+
+
+def seq_layout(t: torch.Tensor, name: str = "tensor") -> SeqLayout:
+    """[B, T, H, 128] bf16 with a contiguous head dim."""
+    _need_cuda(name, t, torch.bfloat16)
+    if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+        raise ValueError(f"{name} must be [B, T, H, {HEAD_DIM}] with a contiguous last dim")
+    return SeqLayout(t.data_ptr(), t.stride(0), t.stride(1), t.stride(2))
+
+
+@dataclass
+class KV:
+    """A K or V tensor plus the way 64-token blocks are addressed in it."""
+
+    tensor: torch.Tensor
+    layout: KvLayout
+    page_table: Optional[torch.Tensor] = None
+
+    @staticmethod
+    def seq_first(t: torch.Tensor) -> "KV":
+        """[B, K, Hkv, 128] (the reference's key_states/value_states)."""
+        _need_cuda("kv", t, torch.bfloat16)
+        if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+            raise ValueError("seq-first KV must be [B, K, Hkv, 128] with a contiguous last dim")
+        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(2), BLOCK * t.stride(1), t.stride(1), None, 0))
+
+    @staticmethod
+    def heads_first(t: torch.Tensor) -> "KV":
+        """[B, Hkv, K, 128] (the reference's k_hf/v_hf cache)."""
+        _need_cuda("kv", t, torch.bfloat16)
+        if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
+            raise ValueError("heads-first KV must be [B, Hkv, K, 128] with a contiguous last dim")
+        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(1), BLOCK * t.stride(2), t.stride(2), None, 0))
+
+    @staticmethod
+    def paged(pool: torch.Tensor, page_table: torch.Tensor) -> "KV":
+        """Global page pool [num_pages, 64, 128] and page_table [B*Hkv, blocks] int32."""
+        _need_cuda("pool", pool, torch.bfloat16)
+        _need_cuda("page_table", page_table, torch.int32)
+        if pool.dim() != 3 or pool.shape[1] != BLOCK or pool.shape[2] != HEAD_DIM or pool.stride(-1) != 1:
+            raise ValueError("page pool must be [num_pages, 64, 128]")
+        if page_table.dim() != 2 or page_table.stride(1) != 1:
+            raise ValueError("page_table must be [rows, blocks] with contiguous rows")
+        return KV(pool, KvLayout(pool.data_ptr(), 0, 0, pool.stride(0), pool.stride(1), page_table.data_ptr(),
+                                 page_table.stride(0)), page_table)
+
+
+def cache_fill(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV, v_cache: KV, past_blocks: Sequence[int],
+               kv_cap: int, kmean: Optional[torch.Tensor], gate_wk: Optional[torch.Tensor] = None,
+               rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
+               kgate: Optional[torch.Tensor] = None) -> None:
+    """Append [B, Lq, Hkv, 128] K/V into the cache at past_blocks; write mean-K (and gate-K)."""
+    B, Lq, Hkv, _ = k_new.shape
+    d = make_dims(B, Lq, Hkv, Hkv, kv_cap)
+    kn = seq_layout(k_new, "k_new")
+    vn = seq_layout(v_new, "v_new")
+    if kmean is not None:
+        _need_cuda("kmean", kmean, torch.float32)
+        if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
+            raise ValueError("kmean must be contiguous [B*Hkv, kv_cap, 128] fp32")
+    rope_rows = 0
+    if gate_wk is not None:
+        _need_cuda("gate_wk", gate_wk, torch.float32)
+        if tuple(gate_wk.shape) != (Hkv, HEAD_DIM, HEAD_DIM) or not gate_wk.is_contiguous():
+            raise ValueError("gate_wk must be contiguous [Hkv, 128, 128] fp32")
+        if kgate is None:
+            raise ValueError("kgate output is required with gate_wk")
+        _need_cuda("kgate", kgate, torch.float32)
+        if rope_cos is not None:
+            _need_cuda("rope_cos", rope_cos, torch.float32)
+            _need_cuda("rope_sin", rope_sin, torch.float32)
+            rope_rows = rope_cos.shape[0]
+    check(_hip.lib().ca_cache_fill(ctypes.byref(d), ctypes.byref(kn), ctypes.byref(vn), ctypes.byref(k_cache.layout),
+                                   ctypes.byref(v_cache.layout), past_array(past_blocks), _ptr(kmean), _ptr(gate_wk),
+                                   _ptr(rope_cos), _ptr(rope_sin), rope_rows, _ptr(kgate), _stream()))
+
+
+def pool_query(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, gate_wq: Optional[torch.Tensor] = None,
+               rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
+               num_kv_heads: Optional[int] = None) -> torch.Tensor:
+    """[B, Lq, Hq, 128] bf16 -> qhat [B, Hq, Lq/64, 128] fp32."""
+    B, Lq, Hq, _ = q.shape
+    d = make_dims(B, Lq, Hq, num_kv_heads or Hq, kv_cap)
+    ql = seq_layout(q, "q")
+    rope_rows = 0
+    if gate_wq is not None:
+        _need_cuda("gate_wq", gate_wq, torch.float32)
+        if tuple(gate_wq.shape) != (Hq, HEAD_DIM, HEAD_DIM) or not gate_wq.is_contiguous():
+            raise ValueError("gate_wq must be contiguous [Hq, 128, 128] fp32")
+        if rope_cos is not None:
+            _need_cuda("rope_cos", rope_cos, torch.float32)
+            _need_cuda("rope_sin", rope_sin, torch.float32)
+            rope_rows = rope_cos.shape[0]
+    qhat = torch.empty((B, Hq, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
+    check(_hip.lib().ca_pool_query(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks), _ptr(gate_wq),
+                                   _ptr(rope_cos), _ptr(rope_sin), rope_rows, qhat.data_ptr(), _stream()))
+    return qhat
+
+
+def words_for(kv_cap: int) -> int:
+    return (kv_cap + 31) // 32
+
+
+def score_select(qhat: torch.Tensor, khat: torch.Tensor, scale: float, rule: Rule, past_blocks: Sequence[int],
+                 num_kv_heads: int, kv_cap: int, with_scores: bool = False
+                 ) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """qhat [B,Hq,Qb,128], khat [B*Hkv, kv_cap, 128] -> rowmask [B,Hq,Qb,words] (+ scores)."""
+    _need_cuda("qhat", qhat, torch.float32)
+    _need_cuda("khat", khat, torch.float32)
+    if not qhat.is_contiguous() or not khat.is_contiguous():
+        raise ValueError("qhat and khat must be contiguous")
+    B, Hq, Qb, _ = qhat.shape
+    if khat.numel() < B * num_kv_heads * kv_cap * HEAD_DIM:
+        raise ValueError("khat smaller than [B*Hkv, kv_cap, 128]")
+    d = make_dims(B, Qb * BLOCK, Hq, num_kv_heads, kv_cap)
+    rowmask = torch.empty((B, Hq, Qb, words_for(kv_cap)), dtype=torch.int32, device=qhat.device)
+    scores = torch.empty((B, Hq, Qb, kv_cap), dtype=torch.float32, device=qhat.device) if with_scores else None
+    r = rule.to_c()
+    check(_hip.lib().ca_score_select(ctypes.byref(d), qhat.data_ptr(), khat.data_ptr(), float(scale), ctypes.byref(r),
+                                     past_array(past_blocks), rowmask.data_ptr(), _ptr(scores), _stream()))
+    return rowmask, scores
+
+
+def select_scores(scores: torch.Tensor, rule: Rule, past_blocks: Sequence[int], num_kv_heads: int, kv_cap: int,
+                  q_len: int) -> torch.Tensor:
+    """Caller scores [B, Hq, Qb, >= P+Qb] (fp32 or bf16, last dim contiguous) -> rowmask."""
+    if not scores.is_cuda:
+        raise ValueError("scores must be a GPU tensor")
+    if scores.dtype == torch.float32:
+        dtype = 0
+    elif scores.dtype == torch.bfloat16:
+        dtype = 1
+    else:
+        raise ValueError(f"scores must be fp32 or bf16 (got {scores.dtype})")
+    if scores.dim() != 4 or scores.stride(-1) != 1:
+        raise ValueError("scores must be [B, Hq, Qb, Kb] with a contiguous last dim")
+    B, Hq, Qb, Kb = scores.shape
+    if Qb != q_len // BLOCK:
+        raise ValueError(f"scores have {Qb} query blocks, expected {q_len // BLOCK}")
+    if Kb < max(int(p) for p in past_blocks) + Qb:
+        raise ValueError("scores have fewer key blocks than past + current blocks")
+    d = make_dims(B, q_len, Hq, num_kv_heads, kv_cap)
+    rowmask = torch.empty((B, Hq, Qb, words_for(kv_cap)), dtype=torch.int32, device=scores.device)
+    r = rule.to_c()
+    check(_hip.lib().ca_select_scores(ctypes.byref(d), scores.data_ptr(), dtype, scores.stride(0), scores.stride(1),
+                                      scores.stride(2), ctypes.byref(r), past_array(past_blocks), rowmask.data_ptr(),
+                                      _stream()))
+    return rowmask
+
+
+def union_compact(rowmask: torch.Tensor, past_blocks: Sequence[int], num_kv_heads: int, kv_cap: int,
+                  last_n_block: int = 0, want_keep_block: bool = False, want_keep_kv: bool = False):
+    """rowmask [B,Hq,Qb,words] -> (table [B*Hkv, kv_cap] i32, counts [B*Hkv] i32, keep_block, keep_kv)."""
+    _need_cuda("rowmask", rowmask, torch.int32)
+    B, Hq, Qb, _ = rowmask.shape
+    d = make_dims(B, Qb * BLOCK, Hq, num_kv_heads, kv_cap)
+    dev = rowmask.device
+    table = torch.empty((B * num_kv_heads, kv_cap), dtype=torch.int32, device=dev)
+    counts = torch.empty((B * num_kv_heads,), dtype=torch.int32, device=dev)
+    keep_block = torch.empty((B, Hq, kv_cap), dtype=torch.uint8, device=dev) if want_keep_block else None
+    keep_kv = torch.empty((B, num_kv_heads, kv_cap), dtype=torch.uint8, device=dev) if want_keep_kv else None
+    check(_hip.lib().ca_union_compact(ctypes.byref(d), rowmask.data_ptr(), int(last_n_block), past_array(past_blocks),
+                                      _ptr(keep_block), _ptr(keep_kv), table.data_ptr(), table.stride(0),
+                                      counts.data_ptr(), _stream()))
+    return table, counts, keep_block, keep_kv
+
+
+def compact_keep_kv(keep_kv: torch.Tensor, past_blocks: Sequence[int], q_len: int, num_q_heads: int,
+                    kv_cap: int) -> Tuple[torch.Tensor, torch.Tensor]:
+    """keep_kv [B, Hkv, kv_cap] u8/bool -> (table, counts); current-chunk blocks always kept."""
+    if keep_kv.dtype == torch.bool:
+        keep_kv = keep_kv.view(torch.uint8)
+    _need_cuda("keep_kv", keep_kv, torch.uint8)
+    B, Hkv, cap = keep_kv.shape
+    if cap != kv_cap or not keep_kv.is_contiguous():
+        raise ValueError("keep_kv must be contiguous [B, Hkv, kv_cap]")
+    d = make_dims(B, q_len, num_q_heads, Hkv, kv_cap)
+    table = torch.empty((B * Hkv, kv_cap), dtype=torch.int32, device=keep_kv.device)
+    counts = torch.empty((B * Hkv,), dtype=torch.int32, device=keep_kv.device)
+    check(_hip.lib().ca_compact_keep_kv(ctypes.byref(d), keep_kv.data_ptr(), past_array(past_blocks),
+                                        table.data_ptr(), table.stride(0), counts.data_ptr(), _stream()))
+    return table, counts
+
+
+def dense_table(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int, kv_cap: int,
+                device) -> Tuple[torch.Tensor, torch.Tensor]:
+    B = len(past_blocks)
+    d = make_dims(B, q_len, num_q_heads, num_kv_heads, kv_cap)
+    table = torch.empty((B * num_kv_heads, kv_cap), dtype=torch.int32, device=device)
+    counts = torch.empty((B * num_kv_heads,), dtype=torch.int32, device=device)
+    check(_hip.lib().ca_dense_table(ctypes.byref(d), past_array(past_blocks), table.data_ptr(), table.stride(0),
+                                    counts.data_ptr(), _stream()))
+    return table, counts
+
+
+def attn_workspace_bytes(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int, kv_cap: int,
+                         num_splits: int = 0) -> int:
+    d = make_dims(len(past_blocks), q_len, num_q_heads, num_kv_heads, kv_cap)
+    n = _hip.lib().ca_attn_workspace_size(ctypes.byref(d), past_array(past_blocks), int(num_splits))
+    if n < 0:
+        raise _hip.CaError(int(n), _hip.last_error())
+    return int(n)
+
+
+def attn_pick_splits(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int,
+                     kv_cap: int) -> int:
+    d = make_dims(len(past_blocks), q_len, num_q_heads, num_kv_heads, kv_cap)
+    n = _hip.lib().ca_attn_pick_splits(ctypes.byref(d), past_array(past_blocks))
+    if n < 0:
+        raise _hip.CaError(int(n), _hip.last_error())
+    return int(n)
+
+
+def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.Tensor, past_blocks: Sequence[int],
+             scale: float, kv_cap: int, num_kv_heads: int, out: Optional[torch.Tensor] = None, with_lse: bool = False,
+             num_splits: int = 0, workspace: Optional[torch.Tensor] = None):
+    """Indexed attention prefill; q/out [B, Lq, Hq, 128] bf16."""
+    B, Lq, Hq, _ = q.shape
+    ql = seq_layout(q, "q")
+    if out is None:
+        out = torch.empty_like(q)
+    ol = seq_layout(out, "out")
+    _need_cuda("table", table, torch.int32)
+    _need_cuda("counts", counts, torch.int32)
+    if table.dim() != 2 or table.stride(1) != 1 or table.shape[0] < B * num_kv_heads:
+        raise ValueError("table must be [B*Hkv, >= kv_cap] with contiguous rows")
+    d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
+    pa = past_array(past_blocks)
+    if num_splits == 0:
+        num_splits = _hip.lib().ca_attn_pick_splits(ctypes.byref(d), pa)
+        if num_splits < 0:
+            raise _hip.CaError(int(num_splits), _hip.last_error())
+    need = _hip.lib().ca_attn_workspace_size(ctypes.byref(d), pa, int(num_splits))
+    if need < 0:
+        raise _hip.CaError(int(need), _hip.last_error())
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need,), dtype=torch.uint8, device=q.device)
+    lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=q.device) if with_lse else None
+    check(_hip.lib().ca_attn_fwd(ctypes.byref(d), ctypes.byref(ql), ctypes.byref(k.layout), ctypes.byref(v.layout),
+                                 table.data_ptr(), table.stride(0), counts.data_ptr(), pa, float(scale),
+                                 ctypes.byref(ol), _ptr(lse), int(num_splits), _ptr(workspace),
+                                 int(need), _stream()))
+    return (out, lse) if with_lse else out

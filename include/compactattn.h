@@ -1,0 +1,219 @@
+/*
+ * compactattn for MI355X (gfx950): C-ABI of libcompactattn_hip.so.
+ *
+ * This library replaces the reference's pybind11 torch extension
+ * `compact_attn._C_compactattn` (compact_attn/csrc/compactattn/cache_fill.cpp:969-1021)
+ * and the third-party / Triton kernels the compactattn prefill path calls around it.
+ *
+ * Conventions
+ *  - Plain pointers to device memory, int sizes and strides (in elements), hipStream_t.
+ *  - Every entry point validates its arguments on the host before any launch and
+ *    returns CA_OK or a negative CA_ERR_* code; ca_last_error() gives the message
+ *    (thread-local).  Nothing allocates device memory; scratch is caller-provided.
+ *  - All launches go to the caller's stream; no entry point synchronises the host.
+ *  - head_dim is 128 and the block (page) size is 64 tokens.
+ *  - bf16 means IEEE bfloat16; summaries and scores are fp32.
+ *
+ * KV addressing.  Element (b, kv_head, logical block kb, token t in block, d) of a K or V
+ * tensor lives at
+ *     data + b*stride_b + kv_head*stride_h + phys(kb)*stride_blk + t*stride_tok + d
+ * with phys(kb) = page_table ? page_table[(b*num_kv_heads + kv_head)*page_table_stride + kb]
+ *                            : kb.
+ * This covers the reference's seq-first [B, K, Hkv, D] tensors, its heads-first
+ * k_hf/v_hf [B, Hkv, K, D] cache (compact_attn/prefill_sparse/llama/
+ * modeling_llama_seerattn_chunked_dense_hf.py:59-82, viewed as 64-token pages by
+ * compact_attn/kernels/varlen/flashinfer_zero_copy_prefill.py:1192-1193) and a global
+ * page pool [num_pages, 64, 128] with a per-row page table.
+ */
+#ifndef COMPACTATTN_H
+#define COMPACTATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CA_ABI_VERSION 1
+#define CA_HEAD_DIM 128
+#define CA_BLOCK 64
+#define CA_MAX_BATCH 64
+
+enum {
+    CA_OK = 0,
+    CA_ERR_INVALID = -1,   /* bad argument (shape, stride, alignment, null pointer) */
+    CA_ERR_LIMIT = -2,     /* a size is beyond what this build supports */
+    CA_ERR_WORKSPACE = -3, /* workspace missing or too small */
+    CA_ERR_HIP = -4        /* a HIP runtime call failed */
+};
+
+/* Selection-rule flags. */
+#define CA_RULE_TOPK 1      /* keep the top-k past blocks by (score desc, block id asc)   */
+#define CA_RULE_ALPHA 2     /* keep score >= alpha * row max (row max over causal, >= 0) */
+#define CA_RULE_THRESHOLD 4 /* keep score > threshold (strict)                           */
+
+typedef struct {
+    int32_t batch;        /* requests in the launch, <= CA_MAX_BATCH                 */
+    int32_t q_len;        /* chunk tokens per request, a multiple of 64              */
+    int32_t num_q_heads;  /* Hq                                                      */
+    int32_t num_kv_heads; /* Hkv; Hq % Hkv == 0, group G = Hq / Hkv <= 16            */
+    int32_t kv_cap;       /* per-row capacity in blocks of tables and summaries;
+                             >= past_blocks[b] + q_len/64 for every request          */
+} ca_dims;
+
+typedef struct {
+    void* data; /* bf16 */
+    int64_t stride_b;
+    int64_t stride_h;
+    int64_t stride_blk;
+    int64_t stride_tok;
+    const int32_t* page_table; /* optional (NULL: physical block = logical block) */
+    int64_t page_table_stride;
+} ca_kv_layout;
+
+typedef struct {
+    void* data; /* bf16, element (b, t, h, d) at data + b*stride_b + t*stride_t + h*stride_h + d */
+    int64_t stride_b;
+    int64_t stride_t;
+    int64_t stride_h;
+} ca_seq_layout;
+
+typedef struct {
+    int32_t flags;         /* CA_RULE_* bits                                          */
+    int32_t topk;          /* blocks per (head, query block) row, over past blocks     */
+    float alpha;           /* CA_RULE_ALPHA factor                                     */
+    float threshold;       /* CA_RULE_THRESHOLD value                                  */
+    int32_t sink_blocks;   /* always keep blocks kb < sink_blocks                      */
+    int32_t window_blocks; /* keep 0 <= (P + qb) - kb < window_blocks                  */
+    int32_t local_blocks;  /* keep the local_blocks past blocks right before the chunk */
+    int32_t last_n_block;  /* leave the last n query blocks out of the union           */
+} ca_select_rule;
+
+/* Library identity and last error (thread-local, valid until the next call). */
+int ca_abi_version(void);
+const char* ca_last_error(void);
+
+/*
+ * Cache fill.  Appends one chunk of K/V per request into the cache at logical blocks
+ * [past_blocks[b], past_blocks[b] + q_len/64) and writes, for each new block, the fp32
+ * mean of its 64 K rows into kmean[(b*Hkv + h)*kv_cap + kb][128] (sequential sum over the
+ * 64 tokens, times 1/64).  If gate_wk is given ([Hkv, 128, 128], in x out) it also writes
+ * kgate = RoPE(W_k[h]^T mean) (rope_cos/rope_sin: [rope_rows, 128] indexed by absolute
+ * block id, may be NULL for no RoPE) into kgate with the kmean layout.
+ * Replaces: transformers DynamicCache.update concatenation
+ * (compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:518-536),
+ * compute_mean_vector / flash_prefill_compute_mean_k
+ * (compact_attn/flashprefill_vendor/flashprefill_native_forward.py:44-95,505-538),
+ * the gate K-block cache append (modeling_llama_seerattn.py:407-435 with
+ * compact_attn/prefill_sparse/attn_gate.py:124-171) and cache_fill_current_tail
+ * (compact_attn/csrc/compactattn/cache_fill.cpp, cache_fill_kernel.cu:665-719).
+ */
+int ca_cache_fill(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_layout* v_new,
+                  const ca_kv_layout* k_cache, const ca_kv_layout* v_cache,
+                  const int32_t* past_blocks_host, float* kmean, const float* gate_wk,
+                  const float* rope_cos, const float* rope_sin, int64_t rope_rows, float* kgate,
+                  void* stream);
+
+/*
+ * Pooled query summaries: qhat[(b*Hq + h)*Qb + qb][128] = mean of the 64 query rows of
+ * block qb (sequential sum, times 1/64), optionally projected by gate_wq [Hq, 128, 128]
+ * and rotated at absolute block id past_blocks[b] + qb.
+ * Replaces: AttnGate.compress_query_blocks + block RoPE (attn_gate.py:113-171) and the
+ * query-side mean of compute_block_score_chunked (flashprefill_native_forward.py:98-207).
+ */
+int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* past_blocks_host,
+                  const float* gate_wq, const float* rope_cos, const float* rope_sin,
+                  int64_t rope_rows, float* qhat, void* stream);
+
+/*
+ * Fused block scoring and per-row selection.  For every (b, h, qb) row it computes
+ * logits[kb] = dot(qhat[b,h,qb], khat[b, h/G, kb]) * scale for kb <= P_b + qb, the softmax
+ * over those kb (fixed evaluation order), applies the rule and writes the row's keep
+ * bitmask rowmask[((b*Hq + h)*Qb + qb)*words + w], words = ceil(kv_cap / 32), bit kb%32 of
+ * word kb/32.  scores_out ([B, Hq, Qb, kv_cap] fp32, non-causal entries 0) is optional.
+ * khat is a kmean/kgate summary array.
+ * Replaces: compute_block_score_chunked + normalize_scores (flashprefill_native_forward.py:
+ * 98-207,365-374), AttnGate.score_compressed_blocks (attn_gate.py:173-204) and the per-row
+ * rules of _flashprefill_keep_block_from_scores_rowwise (compact_attn/modules/
+ * flashprefill_prefill.py:596-666).
+ */
+int ca_score_select(const ca_dims* dims, const float* qhat, const float* khat, float scale,
+                    const ca_select_rule* rule, const int32_t* past_blocks_host, uint32_t* rowmask,
+                    float* scores_out, void* stream);
+
+/*
+ * Per-row selection from caller-provided scores, element (b, h, qb, kb) at
+ * scores + b*stride_b + h*stride_h + qb*stride_q + kb (dtype 0 = fp32, 1 = bf16).  The score
+ * columns cover kb in [0, P_b + Qb); causal as above.  Output as ca_score_select.
+ * Replaces: build_keep_past_fast / build_keep_curr_fast (cache_fill_kernel.cu:274-326,
+ * cache_fill.cpp:1124-1190) and _build_keep_block_mask (compact_attn/modules/
+ * attention_forward_chunked_dense.py:352-403,559-638).
+ */
+int ca_select_scores(const ca_dims* dims, const void* scores, int32_t dtype, int64_t stride_b,
+                     int64_t stride_h, int64_t stride_q, const ca_select_rule* rule,
+                     const int32_t* past_blocks_host, uint32_t* rowmask, void* stream);
+
+/*
+ * Block-Union: Q-block union (OR over query blocks qb < Qb - last_n_block), GQA
+ * intra-group union (OR over the G heads of a KV group), current-chunk blocks always kept,
+ * then ascending compaction.  Writes table[row*table_stride + i] (i < counts[row]) with the
+ * selected logical block ids of row = b*Hkv + kv_head, counts[row], and optionally
+ * keep_block [B, Hq, kv_cap] u8 and keep_kv [B, Hkv, kv_cap] u8 (0/1, zero beyond the row).
+ * Entries of table at i >= counts[row] are set to -1 up to kv_cap.
+ * Replaces: _build_kv_head_union_keep_block_mask (attention_forward_chunked_dense.py:
+ * 641-683), build_past_indices_and_metadata_from_keep_block / build_block_table /
+ * build_selected_indices_from_kv_keep_block / build_flashinfer_kv_indices
+ * (cache_fill_kernel.cu:163-190,328-505) and the Triton union kernel
+ * (flashprefill_prefill.py:307-376).
+ */
+int ca_union_compact(const ca_dims* dims, const uint32_t* rowmask, int32_t last_n_block,
+                     const int32_t* past_blocks_host, uint8_t* keep_block, uint8_t* keep_kv,
+                     int32_t* table, int64_t table_stride, int32_t* counts, void* stream);
+
+/*
+ * Union + compaction from a caller-provided per-KV-group keep mask keep_kv
+ * [B, Hkv, kv_cap] (u8, any nonzero = keep; current-chunk blocks are always kept).
+ * Replaces: build_selected_indices_from_kv_keep_block_out (cache_fill_kernel.cu:449-483)
+ * as used by chunked_prefill_column_dense_attention_from_keep_block
+ * (attention_forward_chunked_dense.py:2147) with keep_block_kv_preprojected.
+ */
+int ca_compact_keep_kv(const ca_dims* dims, const uint8_t* keep_kv, const int32_t* past_blocks_host,
+                       int32_t* table, int64_t table_stride, int32_t* counts, void* stream);
+
+/* Identity tables (every block 0..P_b+Qb-1): the dense full-KV comparator's input. */
+int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t* table,
+                   int64_t table_stride, int32_t* counts, void* stream);
+
+/*
+ * Indexed attention prefill over the selected blocks (bf16 in, fp32 accumulate, bf16 out).
+ * Query token t of request b (absolute position 64*P_b + t) and Q head h attend over the
+ * keys of the blocks table[row][0..counts[row]) of row = b*Hkv + h/G with bottom-right
+ * causal masking (key position j visible iff j <= 64*P_b + t).  out has q's layout;
+ * lse (optional, [B, Hq, q_len] fp32, natural log) receives the log-sum-exp.
+ * num_splits >= 1 splits each row's block list; num_splits > 1 needs a workspace of
+ * ca_attn_workspace_size(dims, num_splits) bytes.  num_splits = 0 picks a split count.
+ * Replaces: flash_attn_with_kvcache / FlashInfer paged prefill as driven by
+ * flash_attn_indexed_prefill_from_paged_kv (compact_attn/kernels/varlen/
+ * indexed_dense_prefill_varlen.py:1473-1613) and flashinfer_prefill_zero_copy
+ * (flashinfer_zero_copy_prefill.py:1139-1353), plus pack_q_for_indexed_prefill
+ * (cache_fill_kernel.cu:130-161) and the selected-KV gathers it needed
+ * (cache_fill_kernel.cu:595-719).
+ */
+int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout* k,
+                const ca_kv_layout* v, const int32_t* table, int64_t table_stride,
+                const int32_t* counts, const int32_t* past_blocks_host, float scale,
+                const ca_seq_layout* out, float* lse, int32_t num_splits, void* workspace,
+                int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes ca_attn_fwd needs for num_splits (0 = the split count it would pick). */
+int64_t ca_attn_workspace_size(const ca_dims* dims, const int32_t* past_blocks_host,
+                               int32_t num_splits);
+
+/* The split count ca_attn_fwd picks when num_splits = 0. */
+int32_t ca_attn_pick_splits(const ca_dims* dims, const int32_t* past_blocks_host);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COMPACTATTN_H */

@@ -1,0 +1,217 @@
+"""CPU oracle for the compactattn chunked-prefill path.
+
+TEST INFRASTRUCTURE ONLY: tests/, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may use this package, and only as the
+checker or the timed CPU baseline.  The product package ``compactattention_amd``
+never imports it.
+
+The numerics live in ``ca_oracle.c`` (fixed fp32 evaluation order, explicit
+fmaf); this module is a numpy front end over ctypes.  bf16 tensors travel as
+``np.uint16`` bit patterns.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libca_oracle.so")
+
+RULE_TOPK = 1
+RULE_ALPHA = 2
+RULE_THRESHOLD = 4
+D = 128
+BLOCK = 64
+
+
+class _Rule(ctypes.Structure):
+    _fields_ = [
+        ("flags", ctypes.c_int32),
+        ("topk", ctypes.c_int32),
+        ("alpha", ctypes.c_float),
+        ("threshold", ctypes.c_float),
+        ("sink_blocks", ctypes.c_int32),
+        ("window_blocks", ctypes.c_int32),
+        ("local_blocks", ctypes.c_int32),
+        ("last_n_block", ctypes.c_int32),
+    ]
+
+
+@dataclass
+class Rule:
+    """Selection rule; field meanings follow the product's ``ca_select_rule``."""
+
+    topk: int = 0
+    alpha: Optional[float] = None
+    threshold: Optional[float] = None
+    sink_blocks: int = 0
+    window_blocks: int = 0
+    local_blocks: int = 0
+    last_n_block: int = 0
+
+    def to_c(self) -> _Rule:
+        flags = 0
+        if self.topk > 0:
+            flags |= RULE_TOPK
+        if self.alpha is not None:
+            flags |= RULE_ALPHA
+        if self.threshold is not None:
+            flags |= RULE_THRESHOLD
+        return _Rule(
+            flags,
+            int(self.topk),
+            float(self.alpha if self.alpha is not None else 0.0),
+            float(self.threshold if self.threshold is not None else 0.0),
+            int(self.sink_blocks),
+            int(self.window_blocks),
+            int(self.local_blocks),
+            int(self.last_n_block),
+        )
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _lib.orc_exp.restype = ctypes.c_float
+        _lib.orc_exp.argtypes = [ctypes.c_float]
+        _lib.orc_num_threads.restype = ctypes.c_int
+    return _lib
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _i32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.int32))
+
+
+def f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even fp32 -> bf16 bit patterns (uint16)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_bits_to_f32(x: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(x, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def exp(x: np.ndarray) -> np.ndarray:
+    f = lib().orc_exp
+    flat = np.asarray(x, dtype=np.float32).ravel()
+    return np.array([f(float(v)) for v in flat], dtype=np.float32).reshape(np.shape(x))
+
+
+def block_mean(x_bits: np.ndarray) -> np.ndarray:
+    """x: [B, L, H, 128] bf16 bits -> [B, H, L/64, 128] fp32 block means."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    B, L, H, d = x.shape
+    assert d == D and L % BLOCK == 0
+    out = np.empty((B, H, L // BLOCK, D), dtype=np.float32)
+    lib().orc_block_mean(_p(x), B, L, H, _p(out))
+    return out
+
+
+def gate_project(x: np.ndarray, W: np.ndarray, cos: Optional[np.ndarray], sin: Optional[np.ndarray],
+                 first_block) -> np.ndarray:
+    """x: [B, H, N, 128] fp32; W: [H, 128, 128]; cos/sin: [rows, 128] by absolute block id."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    B, H, N, _ = x.shape
+    fb = _i32(first_block)
+    y = np.empty_like(x)
+    if cos is None:
+        lib().orc_gate_project(_p(x), B, H, N, _p(W), None, None, ctypes.c_int64(0), _p(fb), _p(y))
+    else:
+        c = np.ascontiguousarray(cos, dtype=np.float32)
+        s = np.ascontiguousarray(sin, dtype=np.float32)
+        lib().orc_gate_project(_p(x), B, H, N, _p(W), _p(c), _p(s), ctypes.c_int64(c.shape[0]),
+                               _p(fb), _p(y))
+    return y
+
+
+def block_scores(qhat: np.ndarray, khat: np.ndarray, past_blocks, scale: float) -> np.ndarray:
+    """qhat [B,Hq,Qb,128], khat [B,Hkv,cap,128] -> softmax-normalised scores [B,Hq,Qb,cap]."""
+    qhat = np.ascontiguousarray(qhat, dtype=np.float32)
+    khat = np.ascontiguousarray(khat, dtype=np.float32)
+    B, Hq, Qb, _ = qhat.shape
+    _, Hkv, cap, _ = khat.shape
+    pb = _i32(past_blocks)
+    out = np.empty((B, Hq, Qb, cap), dtype=np.float32)
+    lib().orc_block_scores(_p(qhat), _p(khat), B, Hq, Hkv, Qb, cap, _p(pb), ctypes.c_float(scale), _p(out))
+    return out
+
+
+def select_rows(scores: np.ndarray, past_blocks, rule: Rule) -> np.ndarray:
+    s = np.ascontiguousarray(scores, dtype=np.float32)
+    B, Hq, Qb, cap = s.shape
+    pb = _i32(past_blocks)
+    out = np.empty((B, Hq, Qb, cap), dtype=np.uint8)
+    r = rule.to_c()
+    lib().orc_select_rows(_p(s), B, Hq, Qb, cap, _p(pb), ctypes.byref(r), _p(out))
+    return out
+
+
+def union_compact(rowkeep: np.ndarray, Hkv: int, past_blocks, last_n_block: int = 0
+                  ) -> Tuple[np.ndarray, np.ndarray, np.ndarray, np.ndarray]:
+    """-> keep_block [B,Hq,cap] u8, keep_kv [B,Hkv,cap] u8, table [B*Hkv,cap] i32, counts [B*Hkv]."""
+    rk = np.ascontiguousarray(rowkeep, dtype=np.uint8)
+    B, Hq, Qb, cap = rk.shape
+    pb = _i32(past_blocks)
+    keep_block = np.empty((B, Hq, cap), dtype=np.uint8)
+    keep_kv = np.empty((B, Hkv, cap), dtype=np.uint8)
+    table = np.empty((B * Hkv, cap), dtype=np.int32)
+    counts = np.empty((B * Hkv,), dtype=np.int32)
+    lib().orc_union_compact(_p(rk), B, Hq, Hkv, Qb, cap, _p(pb), int(last_n_block), _p(keep_block),
+                            _p(keep_kv), _p(table), _p(counts))
+    return keep_block, keep_kv, table, counts
+
+
+def attention(q_bits: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, past_blocks, table: np.ndarray,
+              counts: np.ndarray, scale: float, q_range: Optional[Tuple[int, int]] = None,
+              head_range: Optional[Tuple[int, int]] = None, with_lse: bool = False):
+    """q [B,Lq,Hq,128] bf16 bits; k,v [B,Hkv,cap*64,128] bf16 bits heads-first.
+
+    Returns out [B,Lq,Hq,128] fp32 (and lse [B,Hq,Lq] if requested).  Entries outside
+    q_range / head_range are NaN.
+    """
+    q = np.ascontiguousarray(q_bits, dtype=np.uint16)
+    k = np.ascontiguousarray(k_bits, dtype=np.uint16)
+    v = np.ascontiguousarray(v_bits, dtype=np.uint16)
+    B, Lq, Hq, _ = q.shape
+    _, Hkv, ktok, _ = k.shape
+    cap = ktok // BLOCK
+    tab = np.ascontiguousarray(table, dtype=np.int32)
+    assert tab.shape[1] == cap, "table stride must equal the KV capacity in blocks"
+    cnt = _i32(counts)
+    pb = _i32(past_blocks)
+    q0, q1 = q_range if q_range is not None else (0, Lq)
+    h0, h1 = head_range if head_range is not None else (0, Hq)
+    out = np.full((B, Lq, Hq, D), np.nan, dtype=np.float32)
+    lse = np.full((B, Hq, Lq), np.nan, dtype=np.float32) if with_lse else None
+    lib().orc_attention(_p(q), _p(k), _p(v), B, Lq, Hq, Hkv, cap, _p(pb), _p(tab), _p(cnt),
+                        ctypes.c_float(scale), q0, q1, h0, h1, _p(out),
+                        _p(lse) if lse is not None else None)
+    return (out, lse) if with_lse else out
+
+
+def num_threads() -> int:
+    return int(lib().orc_num_threads())

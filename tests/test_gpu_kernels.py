@@ -1,0 +1,281 @@
+"""GPU parity of every C-ABI entry point against the CPU oracle.
+
+Bit-exact: cache copy, mean-K / gate-K summaries, pooled Q, fp32 block scores, per-row
+selection masks, unions, block tables and counts.  Tolerance (north star): attention
+output in bf16 within max-abs 2e-2 and mean-abs 2e-3 of the fp64-accumulated oracle over
+the same selected blocks.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from compactattention_amd import ops
+from compactattention_amd.synthetic import make_chunk, rope_tables
+
+from .util import bits, f32, float_bits_equal, pack_rowmask, unpack_rowmask
+
+pytestmark = pytest.mark.gpu
+
+ATOL_MAX = 2e-2
+ATOL_MEAN = 2e-3
+
+
+def _print_case(**kw):
+    print("case:", ", ".join(f"{k}={v}" for k, v in kw.items()), flush=True)
+
+
+# ----------------------------------------------------------------------------- cache fill
+@pytest.mark.parametrize("layout", ["heads_first", "seq_first", "paged"])
+@pytest.mark.parametrize("gate", [False, True])
+def test_cache_fill_bit_exact(gpu, layout, gate):
+    _print_case(test="cache_fill", layout=layout, gate=gate)
+    B, Lq, Hkv, past = 2, 256, 3, [5, 9]
+    qb = Lq // 64
+    cap = max(past) + qb + 2
+    g = torch.Generator().manual_seed(7)
+    k_new = torch.randn((B, Lq, Hkv, 128), generator=g).to(torch.bfloat16)
+    v_new = torch.randn((B, Lq, Hkv, 128), generator=g).to(torch.bfloat16)
+    wk = (torch.randn((Hkv, 128, 128), generator=g) * 0.02).float()
+    cos, sin = rope_tables(cap)
+    if layout == "heads_first":
+        kc = torch.zeros((B, Hkv, cap * 64, 128), dtype=torch.bfloat16, device=gpu)
+        vc = torch.zeros_like(kc)
+        K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+    elif layout == "seq_first":
+        kc = torch.zeros((B, cap * 64, Hkv, 128), dtype=torch.bfloat16, device=gpu)
+        vc = torch.zeros_like(kc)
+        K, V = ops.KV.seq_first(kc), ops.KV.seq_first(vc)
+    else:
+        rows = B * Hkv
+        perm = torch.randperm(rows * cap, generator=g).to(torch.int32)
+        pt = perm.view(rows, cap).contiguous().to(gpu)
+        kc = torch.zeros((rows * cap, 64, 128), dtype=torch.bfloat16, device=gpu)
+        vc = torch.zeros_like(kc)
+        K, V = ops.KV.paged(kc, pt), ops.KV.paged(vc, pt)
+    kmean = torch.full((B * Hkv, cap, 128), float("nan"), device=gpu)
+    kgate = torch.full((B * Hkv, cap, 128), float("nan"), device=gpu) if gate else None
+    ops.cache_fill(k_new.to(gpu), v_new.to(gpu), K, V, past, cap, kmean,
+                   gate_wk=wk.to(gpu) if gate else None, rope_cos=cos.to(gpu) if gate else None,
+                   rope_sin=sin.to(gpu) if gate else None, kgate=kgate)
+    torch.cuda.synchronize()
+    # copy: every new block lands at its logical position
+    for b in range(B):
+        for h in range(Hkv):
+            for j in range(qb):
+                kb = past[b] + j
+                if layout == "heads_first":
+                    got_k = kc[b, h, kb * 64:(kb + 1) * 64]
+                    got_v = vc[b, h, kb * 64:(kb + 1) * 64]
+                elif layout == "seq_first":
+                    got_k = kc[b, kb * 64:(kb + 1) * 64, h]
+                    got_v = vc[b, kb * 64:(kb + 1) * 64, h]
+                else:
+                    page = int(pt[b * Hkv + h, kb])
+                    got_k, got_v = kc[page], vc[page]
+                assert torch.equal(got_k.cpu(), k_new[b, j * 64:(j + 1) * 64, h])
+                assert torch.equal(got_v.cpu(), v_new[b, j * 64:(j + 1) * 64, h])
+    means = oracle.block_mean(bits(k_new))  # [B, Hkv, qb, 128]
+    km = f32(kmean).reshape(B, Hkv, cap, 128)
+    for b in range(B):
+        assert float_bits_equal(km[b, :, past[b]:past[b] + qb], means[b])
+    if gate:
+        kg = f32(kgate).reshape(B, Hkv, cap, 128)
+        ref = oracle.gate_project(means, f32(wk), f32(cos), f32(sin), past)
+        for b in range(B):
+            assert float_bits_equal(kg[b, :, past[b]:past[b] + qb], ref[b])
+
+
+# ----------------------------------------------------------------------------- pooled Q
+@pytest.mark.parametrize("gate", [False, True])
+def test_pool_query_bit_exact(gpu, gate):
+    _print_case(test="pool_query", gate=gate)
+    B, Lq, Hq, past = 2, 192, 5, [0, 7]
+    g = torch.Generator().manual_seed(11)
+    q = torch.randn((B, Lq, Hq, 128), generator=g).to(torch.bfloat16)
+    wq = (torch.randn((Hq, 128, 128), generator=g) * 0.02).float()
+    cap = max(past) + Lq // 64
+    cos, sin = rope_tables(cap)
+    qhat = ops.pool_query(q.to(gpu), past, cap, gate_wq=wq.to(gpu) if gate else None,
+                          rope_cos=cos.to(gpu) if gate else None, rope_sin=sin.to(gpu) if gate else None)
+    ref = oracle.block_mean(bits(q))
+    if gate:
+        ref = oracle.gate_project(ref, f32(wq), f32(cos), f32(sin), past)
+    assert float_bits_equal(f32(qhat), ref)
+
+
+# ----------------------------------------------------------------------------- scoring + selection
+RULES = {
+    "topk_sink_local": oracle.Rule(topk=5, sink_blocks=1, local_blocks=2),
+    "alpha_sink_window": oracle.Rule(alpha=0.06, sink_blocks=2, window_blocks=4),
+    "threshold": oracle.Rule(threshold=5e-3, sink_blocks=1, local_blocks=2),
+    "topk_alpha": oracle.Rule(topk=3, alpha=0.5),
+    "topk_ge_candidates": oracle.Rule(topk=1000),
+}
+
+
+def _ops_rule(r: oracle.Rule) -> ops.Rule:
+    return ops.Rule(topk=r.topk, alpha=r.alpha, threshold=r.threshold, sink_blocks=r.sink_blocks,
+                    window_blocks=r.window_blocks, local_blocks=r.local_blocks, last_n_block=r.last_n_block)
+
+
+@pytest.mark.parametrize("rule_name", sorted(RULES))
+@pytest.mark.parametrize("G", [1, 4, 7])
+def test_score_select_bit_exact(gpu, rule_name, G):
+    rule = RULES[rule_name]
+    _print_case(test="score_select", rule=rule_name, G=G)
+    B, Hkv, Lq = 2, 2, 256
+    Hq = Hkv * G
+    past = [37, 70]
+    cap = max(past) + Lq // 64 + 3
+    g = torch.Generator().manual_seed(100 + G)
+    qhat = torch.randn((B, Hq, Lq // 64, 128), generator=g) * 0.3
+    khat = torch.randn((B * Hkv, cap, 128), generator=g) * 0.3
+    scale = 1.0 / math.sqrt(128)
+    rowmask, scores = ops.score_select(qhat.to(gpu), khat.to(gpu), scale, _ops_rule(rule), past, Hkv, cap,
+                                       with_scores=True)
+    ref_scores = oracle.block_scores(qhat.numpy(), khat.numpy().reshape(B, Hkv, cap, 128), past, scale)
+    assert float_bits_equal(f32(scores), ref_scores)
+    ref_keep = oracle.select_rows(ref_scores, past, rule)
+    assert np.array_equal(unpack_rowmask(rowmask, cap), ref_keep)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_select_scores_ties_and_nonfinite(gpu, dtype):
+    _print_case(test="select_scores", dtype=dtype)
+    B, Hkv, G, Lq = 1, 2, 3, 128
+    Hq = Hkv * G
+    past = [50]
+    qb = Lq // 64
+    cap = 64
+    g = torch.Generator().manual_seed(3)
+    # few distinct values -> many ties; sprinkle -inf / nan / +inf / -0.0
+    s = torch.randint(0, 4, (B, Hq, qb, cap), generator=g).float() * 0.25
+    s[..., 3] = float("-inf")
+    s[0, 1, 0, 7] = float("nan")
+    s[0, 2, 1, 9] = float("inf")
+    s[0, 0, 0, 11] = -0.0
+    s = s.to(dtype)
+    for rule in (oracle.Rule(topk=6), oracle.Rule(topk=6, alpha=0.9), oracle.Rule(threshold=0.3, sink_blocks=1)):
+        rowmask = ops.select_scores(s.to(gpu), _ops_rule(rule), past, Hkv, cap, Lq)
+        ref = oracle.select_rows(s.float().numpy(), past, rule)
+        assert np.array_equal(unpack_rowmask(rowmask, cap), ref), rule
+
+
+# ----------------------------------------------------------------------------- union + tables
+@pytest.mark.parametrize("last_n_block", [0, 2])
+@pytest.mark.parametrize("G", [1, 4, 7])
+def test_union_compact_bit_exact(gpu, G, last_n_block):
+    _print_case(test="union_compact", G=G, last_n_block=last_n_block)
+    B, Hkv, Lq = 3, 2, 256
+    Hq = Hkv * G
+    past = [0, 33, 95]
+    qb = Lq // 64
+    cap = max(past) + qb + 5
+    g = torch.Generator().manual_seed(G)
+    rowkeep = (torch.rand((B, Hq, qb, cap), generator=g) < 0.05).to(torch.uint8).numpy()
+    for b in range(B):  # the selection never marks non-causal entries
+        for q in range(qb):
+            rowkeep[b, :, q, past[b] + q + 1:] = 0
+    rm = pack_rowmask(rowkeep, cap)
+    rowmask = torch.from_numpy(rm.view(np.int32)).to(gpu)
+    table, counts, keep_block, keep_kv = ops.union_compact(rowmask, past, Hkv, cap, last_n_block=last_n_block,
+                                                            want_keep_block=True, want_keep_kv=True)
+    ref_kb, ref_kv, ref_tab, ref_cnt = oracle.union_compact(rowkeep, Hkv, past, last_n_block)
+    assert np.array_equal(counts.cpu().numpy(), ref_cnt)
+    assert np.array_equal(table.cpu().numpy(), ref_tab)
+    assert np.array_equal(keep_block.cpu().numpy(), ref_kb)
+    assert np.array_equal(keep_kv.cpu().numpy(), ref_kv)
+    # the caller-mask entry point reproduces the same table from keep_kv
+    t2, c2 = ops.compact_keep_kv(torch.from_numpy(ref_kv).to(gpu), past, Lq, Hq, cap)
+    assert np.array_equal(c2.cpu().numpy(), ref_cnt)
+    assert np.array_equal(t2.cpu().numpy(), ref_tab)
+
+
+def test_dense_table(gpu):
+    past = [0, 3, 17]
+    t, c = ops.dense_table(past, 128, 8, 2, 24, gpu)
+    t, c = t.cpu().numpy(), c.cpu().numpy()
+    for b, P in enumerate(past):
+        for h in range(2):
+            r = b * 2 + h
+            assert c[r] == P + 2
+            assert np.array_equal(t[r, :P + 2], np.arange(P + 2))
+            assert (t[r, P + 2:] == -1).all()
+
+
+# ----------------------------------------------------------------------------- attention
+def _attn_case(gpu, past_tokens, Lq, Hq, Hkv, layout, splits, keep_frac, seed):
+    ch = make_chunk(past_tokens, Lq, Hq, Hkv, seed=seed, planted_blocks=2)
+    B = len(past_tokens)
+    cap = ch.kv_cap
+    g = torch.Generator().manual_seed(seed + 1)
+    keep_kv = (torch.rand((B, Hkv, cap), generator=g) < keep_frac).to(torch.uint8)
+    qg, kg, vg = ch.q.to(gpu), ch.k.to(gpu), ch.v.to(gpu)
+    table, counts = ops.compact_keep_kv(keep_kv.to(gpu), ch.past_blocks, Lq, Hq, cap)
+    if layout == "heads_first":
+        K, V = ops.KV.heads_first(kg), ops.KV.heads_first(vg)
+    elif layout == "seq_first":
+        K, V = ops.KV.seq_first(kg.transpose(1, 2).contiguous()), ops.KV.seq_first(vg.transpose(1, 2).contiguous())
+    else:
+        rows = B * Hkv
+        perm = torch.randperm(rows * cap, generator=g).to(torch.int32).view(rows, cap)
+        pool_k = torch.empty((rows * cap, 64, 128), dtype=torch.bfloat16)
+        pool_v = torch.empty_like(pool_k)
+        kc, vc = ch.k.view(rows, cap, 64, 128), ch.v.view(rows, cap, 64, 128)
+        pool_k[perm.view(-1).long()] = kc.reshape(rows * cap, 64, 128)
+        pool_v[perm.view(-1).long()] = vc.reshape(rows * cap, 64, 128)
+        K, V = ops.KV.paged(pool_k.to(gpu), perm.to(gpu)), ops.KV.paged(pool_v.to(gpu), perm.to(gpu))
+    scale = 1.0 / math.sqrt(128)
+    out, lse = ops.attn_fwd(qg, K, V, table, counts, ch.past_blocks, scale, cap, Hkv, with_lse=True,
+                            num_splits=splits)
+    torch.cuda.synchronize()
+    ref, ref_lse = oracle.attention(bits(ch.q), bits(ch.k), bits(ch.v), ch.past_blocks, table.cpu().numpy(),
+                                    counts.cpu().numpy(), scale, with_lse=True)
+    got = f32(out)
+    err = np.abs(got - ref)
+    assert np.isfinite(got).all()
+    assert err.max() <= ATOL_MAX, err.max()
+    assert err.mean() <= ATOL_MEAN, err.mean()
+    lerr = np.abs(f32(lse) - ref_lse)
+    assert lerr.max() <= 1e-3, lerr.max()
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3])
+@pytest.mark.parametrize("layout", ["heads_first", "seq_first", "paged"])
+def test_attention_layouts_and_splits(gpu, layout, splits):
+    _print_case(test="attention", layout=layout, splits=splits)
+    _attn_case(gpu, [64 * 40], 256, 8, 2, layout, splits, 0.3, seed=21)
+
+
+@pytest.mark.parametrize("G,Lq", [(1, 128), (4, 320), (7, 256), (8, 192)])
+def test_attention_groups(gpu, G, Lq):
+    _print_case(test="attention_groups", G=G, Lq=Lq)
+    _attn_case(gpu, [64 * 23], Lq, 2 * G, 2, "heads_first", 0, 0.4, seed=31 + G)
+
+
+def test_attention_ragged_batch(gpu):
+    _print_case(test="attention_ragged")
+    _attn_case(gpu, [0, 64 * 5, 64 * 31, 64 * 12], 128, 14, 2, "heads_first", 0, 0.25, seed=41)
+
+
+def test_attention_all_selected_equals_dense(gpu):
+    """Keeping every block reduces to dense causal attention (checked against torch fp32 SDPA)."""
+    _print_case(test="attention_dense")
+    past_tok, Lq, Hq, Hkv = 64 * 12, 128, 4, 2
+    ch = make_chunk([past_tok], Lq, Hq, Hkv, seed=5, planted_blocks=0)
+    table, counts = ops.dense_table(ch.past_blocks, Lq, Hq, Hkv, ch.kv_cap, gpu)
+    out = ops.attn_fwd(ch.q.to(gpu), ops.KV.heads_first(ch.k.to(gpu)), ops.KV.heads_first(ch.v.to(gpu)),
+                       table, counts, ch.past_blocks, 1 / math.sqrt(128), ch.kv_cap, Hkv)
+    K = past_tok + Lq
+    q = ch.q.float().permute(0, 2, 1, 3)  # [1, Hq, Lq, D]
+    k = ch.k[:, :, :K].float().repeat_interleave(Hq // Hkv, dim=1)
+    v = ch.v[:, :, :K].float().repeat_interleave(Hq // Hkv, dim=1)
+    mask = torch.arange(K)[None, :] <= (past_tok + torch.arange(Lq))[:, None]
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask).permute(0, 2, 1, 3)
+    err = (out.float().cpu() - ref).abs()
+    assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
