@@ -78,3 +78,39 @@ def rope_tables(num_rows: int, dim: int = HEAD_DIM, theta: float = 500000.0, str
     freqs = pos[:, None] * inv_freq[None, :]
     emb = torch.cat([freqs, freqs], dim=-1)
     return emb.cos().to(torch.float32), emb.sin().to(torch.float32)
+
+
+def make_chunk_device(past_tokens: int, q_len: int, num_q_heads: int, num_kv_heads: int, device,
+                      seed: int = DEFAULT_SEED, planted_blocks: int = 8, plant_scale: float = 2.0,
+                      local_blocks: int = 2, kv_cap: int = 0) -> ChunkInputs:
+    """Single-request inputs generated on the GPU (large configurations); same structure
+    as make_chunk, drawn from a device generator."""
+    if q_len % BLOCK or past_tokens % BLOCK:
+        raise ValueError("lengths must be multiples of 64")
+    P = past_tokens // BLOCK
+    qb = q_len // BLOCK
+    cap = max(kv_cap, P + qb)
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    u = torch.randn(HEAD_DIM, generator=g, device=device)
+    u = u / u.norm()
+    q = torch.randn((1, q_len, num_q_heads, HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    k = torch.empty((1, num_kv_heads, cap * BLOCK, HEAD_DIM), dtype=torch.bfloat16, device=device)
+    v = torch.empty_like(k)
+    for h in range(num_kv_heads):  # per head to bound the fp32 temporaries
+        k[0, h] = torch.randn((cap * BLOCK, HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+        v[0, h] = torch.randn((cap * BLOCK, HEAD_DIM), generator=g, device=device).to(torch.bfloat16)
+    planted: List[List[int]] = []
+    lo, hi = 1, P - local_blocks
+    for h in range(num_kv_heads):
+        ids = []
+        if hi - lo >= planted_blocks and planted_blocks > 0:
+            ids = (torch.randperm(hi - lo, generator=g, device=device)[:planted_blocks] + lo).sort().values.tolist()
+        for blk in ids:
+            seg = k[0, h, blk * BLOCK:(blk + 1) * BLOCK]
+            seg.copy_((seg.float() + plant_scale * u).to(torch.bfloat16))
+        planted.append(ids)
+    live = (P + qb) * BLOCK
+    k[:, :, live:] = 0
+    v[:, :, live:] = 0
+    return ChunkInputs(q, k, v, [P], cap, [planted])
