@@ -186,19 +186,19 @@ int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* pa
 
 int ca_score_select(const ca_dims* dims, const float* qhat, const float* khat, float scale,
                     const ca_select_rule* rule, const int32_t* past_blocks_host, uint32_t* rowmask,
-                    float* scores_out, void* stream) {
+                    float* scores, void* stream) {
     ca::Shape s;
     ca::PastBlocks pb;
     int max_nkb = 0, rc;
     if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
     if ((rc = check_rule(rule)) != CA_OK) return rc;
-    if (qhat == nullptr || khat == nullptr || rowmask == nullptr)
-        return fail(CA_ERR_INVALID, "qhat, khat and rowmask are required");
-    if (!aligned16(khat)) return fail(CA_ERR_INVALID, "khat must be 16-byte aligned");
+    if (qhat == nullptr || khat == nullptr || rowmask == nullptr || scores == nullptr)
+        return fail(CA_ERR_INVALID, "qhat, khat, rowmask and scores are required");
+    if (!aligned16(khat) || !aligned16(qhat)) return fail(CA_ERR_INVALID, "qhat and khat must be 16-byte aligned");
     if (ca::score_select_lds_bytes(s, true) > kMaxLds)
         return fail(CA_ERR_LIMIT, "group %d x kv_cap %d scores do not fit in LDS", s.G, s.cap);
     hipError_t e = ca::launch_score_select(s, qhat, khat, scale, nullptr, 0, 0, 0, 0, *rule, pb, rowmask,
-                                           scores_out, static_cast<hipStream_t>(stream));
+                                           scores, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "score_select launch");
     return ok();
 }
@@ -233,7 +233,7 @@ int ca_union_compact(const ca_dims* dims, const uint32_t* rowmask, int32_t last_
     if (rowmask == nullptr || table == nullptr || counts == nullptr)
         return fail(CA_ERR_INVALID, "rowmask, table and counts are required");
     if (table_stride < s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, s.cap);
-    if (sizeof(uint32_t) * (size_t)s.words > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
+    if (ca::union_lds_bytes(s) > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
     hipError_t e = ca::launch_union_compact(s, rowmask, last_n_block, nullptr, pb, keep_block, keep_kv, table,
                                             table_stride, counts, false, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "union_compact launch");
@@ -249,7 +249,7 @@ int ca_compact_keep_kv(const ca_dims* dims, const uint8_t* keep_kv, const int32_
     if (keep_kv == nullptr || table == nullptr || counts == nullptr)
         return fail(CA_ERR_INVALID, "keep_kv, table and counts are required");
     if (table_stride < s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, s.cap);
-    if (sizeof(uint32_t) * (size_t)s.words > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
+    if (ca::union_lds_bytes(s) > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
     hipError_t e = ca::launch_union_compact(s, nullptr, 0, keep_kv, pb, nullptr, nullptr, table, table_stride,
                                             counts, false, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "compact_keep_kv launch");
@@ -264,7 +264,7 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
     if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
     if (table == nullptr || counts == nullptr) return fail(CA_ERR_INVALID, "table and counts are required");
     if (table_stride < s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, s.cap);
-    if (sizeof(uint32_t) * (size_t)s.words > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
+    if (ca::union_lds_bytes(s) > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap too large");
     hipError_t e = ca::launch_union_compact(s, nullptr, 0, nullptr, pb, nullptr, nullptr, table, table_stride,
                                             counts, true, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "dense_table launch");

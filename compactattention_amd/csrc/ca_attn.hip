@@ -38,8 +38,13 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
-constexpr int kBM = 256;             // packed query rows per workgroup
-constexpr int kKvBytes = 64 * 128 * 2;  // one 64-token K or V block in bf16
+constexpr int kNW = 4;               // waves per workgroup (32 packed query rows each)
+constexpr int kBM = 32 * kNW;        // packed query rows per workgroup
+constexpr int kKPitch = 272;  // bytes per K row in LDS (256 + 16 pad: conflict-free fragment reads)
+constexpr int kVPitch = 128;  // bytes per V^T row in LDS (16-byte chunks XOR-swizzled by row)
+constexpr int kKBytes = 64 * kKPitch;
+constexpr int kVBytes = 128 * kVPitch;
+constexpr int kStageBytes = kKBytes + kVBytes;
 constexpr float kRescale = 8.0f;      // lazy-rescale slack (log2 units)
 
 struct AttnParams {
@@ -74,8 +79,14 @@ __device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
 }
 
 
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2][2][kKvBytes];  // [stage][K, V^T]
+// NW waves per workgroup, 32 packed query rows per wave (one 32x32 MFMA row tile), so a
+// workgroup owns BM = 32*NW rows.  Registers stay within 256 per lane, which lets two waves
+// share a SIMD: one wave's softmax overlaps the other's MFMAs.
+template <int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fwd_kernel(AttnParams p) {
+    constexpr int BM = 32 * NW;
+    constexpr int NT = NW * 64;
+    __shared__ __attribute__((aligned(16))) uint8_t smem[2][kStageBytes];  // [stage]: K rows, then V^T rows
 
     const int L = blockIdx.x;
     const int W = (L & 7) * p.per_xcd + (L >> 3);
@@ -90,9 +101,9 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
     const int G = s.G;
     const int P = p.pb.p[b];
     const int rows_total = p.rows_total;
-    const int r0 = tile * kBM;
+    const int r0 = tile * BM;
     const int t_first = r0 / G;
-    const int t_last = min(r0 + kBM - 1, rows_total - 1) / G;
+    const int t_last = min(r0 + BM - 1, rows_total - 1) / G;
 
     const int32_t* tab = p.table + (int64_t)row * p.table_stride;
     const int nkb = P + s.Qb;  // valid logical block ids are [0, nkb)
@@ -103,6 +114,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
     const int chunk = (n_vis + p.splits - 1) / p.splits;
     const int e0 = min(n_vis, split * chunk);
     const int e1 = min(n_vis, e0 + chunk);
+    // table entries are clamped into [0, nkb) so a corrupt table cannot address outside
+    // the KV tensors
+    auto block_id = [&](int e) { return min(max(tab[e], 0), nkb - 1); };
+    // entries at or after e_mask contain keys beyond the tile's first query position
+    int e_mask = e1;
+    while (e_mask > e0 && block_id(e_mask - 1) * 64 + 63 > P * 64 + t_first) --e_mask;
 
     const int tid = threadIdx.x;
     const int w = tid >> 6;
@@ -111,221 +128,210 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
     const int n = l & 31;
 
     // ---- Q fragments (B operand of S^T = K Q^T) ----
-    bf16x8_t qf[2][8];
-    int qtok[2];
-    int qg[2];
-    bool qvalid[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const int r = r0 + 64 * w + 32 * rt + n;
-        qvalid[rt] = r < rows_total;
-        const int t = qvalid[rt] ? r / G : 0;
-        const int g = qvalid[rt] ? r - t * G : 0;
-        qtok[rt] = qvalid[rt] ? t : 0x3fffffff;
-        qg[rt] = g;
-        const uint16_t* qp = p.q.data + b * p.q.sb + (int64_t)t * p.q.st + (int64_t)(hk * G + g) * p.q.sh + 8 * h;
+    const int qrow = r0 + 32 * w + n;
+    const bool qvalid = qrow < rows_total;
+    const int qt = qvalid ? qrow / G : 0;
+    const int qg = qvalid ? qrow - qt * G : 0;
+    bf16x8_t qf[8];
+    {
+        const uint16_t* qp = p.q.data + b * p.q.sb + (int64_t)qt * p.q.st + (int64_t)(hk * G + qg) * p.q.sh + 8 * h;
 #pragma unroll
         for (int ds = 0; ds < 8; ++ds) {
-            if (qvalid[rt]) {
-                qf[rt][ds] = *reinterpret_cast<const bf16x8_t*>(qp + 16 * ds);
+            if (qvalid) {
+                qf[ds] = *reinterpret_cast<const bf16x8_t*>(qp + 16 * ds);
             } else {
                 u32x4_t z = {0u, 0u, 0u, 0u};
-                qf[rt][ds] = __builtin_bit_cast(bf16x8_t, z);
+                qf[ds] = __builtin_bit_cast(bf16x8_t, z);
             }
         }
     }
+    const int qtok = qvalid ? qt : 0x3fffffff;
 
-    f32x16_t oacc[4][2];
+    f32x16_t oacc[4];
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-            for (int j = 0; j < 16; ++j) oacc[dt][rt][j] = 0.0f;
-    float m_run[2] = {-__builtin_inff(), -__builtin_inff()};
-    float l_run[2] = {0.0f, 0.0f};
+        for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.0f;
+    float m_run = -__builtin_inff();
+    float l_run = 0.0f;
 
     const uint16_t* kbase_row = p.k.data + b * p.k.sb + hk * p.k.sh;
     const uint16_t* vbase_row = p.v.data + b * p.v.sb + hk * p.v.sh;
     const int32_t* kpt = p.k.page_table ? p.k.page_table + (int64_t)row * p.k.pts : nullptr;
     const int32_t* vpt = p.v.page_table ? p.v.page_table + (int64_t)row * p.v.pts : nullptr;
 
-    // per-thread global->LDS assignment; 32-bit element offsets inside one 64-token block
-    // (the host checks 64 * stride_tok < 2^30) on top of a wave-uniform block base
-    const int k_key0 = tid >> 4;      // + 16*i
-    const int k_chunk = tid & 15;
-    const int v_kg = tid >> 5;        // keys 8*v_kg .. +7
-    const int v_dg = tid & 31;        // d 4*v_dg .. +3
-    const uint32_t kstok = static_cast<uint32_t>(p.k.stok);
-    const uint32_t vstok = static_cast<uint32_t>(p.v.stok);
-    const uint32_t k_off0 = static_cast<uint32_t>(k_key0) * kstok + 8u * k_chunk;
-    const uint32_t v_off0 = static_cast<uint32_t>(8 * v_kg) * vstok + 4u * v_dg;
-
+    // ---- global -> LDS staging of one block ----
+    // With 256 threads every thread moves 4 x 16 B of K and 8 x 8 B of V; with 512 threads
+    // the first half moves K and the second half V.  32-bit element offsets inside a block
+    // (the host checks 64 * stride_tok < 2^30) on top of a wave-uniform block base.
+    constexpr bool kSplitKV = NT >= 512;
+    const int kt_id = kSplitKV ? (tid & 255) : tid;
+    const bool does_k = !kSplitKV || tid < 256;
+    const bool does_v = !kSplitKV || tid >= 256;
+    const int k_key0 = kt_id >> 4;  // + 16*i
+    const int k_chunk = kt_id & 15;
+    const int v_kg = kt_id >> 5;
+    const int v_dg = kt_id & 31;
+    // Loads go through buffer resources built per block (wave-uniform base in SGPRs), so a
+    // lane needs one 32-bit offset register per tensor; the per-row/per-key strides ride in
+    // the scalar offset.
+    const int kstok_b = static_cast<int>(p.k.stok) * 2;
+    const int vstok_b = static_cast<int>(p.v.stok) * 2;
+    const int k_voff = k_key0 * kstok_b + 16 * k_chunk;
+    const int v_voff = 8 * v_kg * vstok_b + 8 * v_dg;
     u32x4_t kreg[4];
     u32x2_t vreg[8];
-
-    // table entries are clamped into [0, nkb) so a corrupt table cannot address outside
-    // the KV tensors
-    auto block_id = [&](int e) { return min(max(tab[e], 0), nkb - 1); };
     auto load_block = [&](int e) {
         const int kb = block_id(e);
-        const int64_t kphys = kpt ? kpt[kb] : kb;
-        const int64_t vphys = vpt ? vpt[kb] : kb;
-        const uint16_t* kb_ptr = kbase_row + kphys * p.k.sblk;
-        const uint16_t* vb_ptr = vbase_row + vphys * p.v.sblk;
+        if (does_k) {
+            const int64_t kphys = kpt ? kpt[kb] : kb;
+            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(kbase_row + kphys * p.k.sblk), 0, 0x7fffffff, 0x00020000);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            kreg[i] = *reinterpret_cast<const u32x4_t*>(kb_ptr + (k_off0 + static_cast<uint32_t>(i) * 16u * kstok));
+            for (int i = 0; i < 4; ++i)
+                kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_voff, i * 16 * kstok_b, 0);
+        }
+        if (does_v) {
+            const int64_t vphys = vpt ? vpt[kb] : kb;
+            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<uint16_t*>(vbase_row + vphys * p.v.sblk), 0, 0x7fffffff, 0x00020000);
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
-            vreg[r] = *reinterpret_cast<const u32x2_t*>(vb_ptr + (v_off0 + static_cast<uint32_t>(r) * vstok));
+            for (int r = 0; r < 8; ++r) vreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rv, v_voff, r * vstok_b, 0);
+        }
     };
     auto store_block = [&](int stage) {
-        uint8_t* ks = smem[stage][0];
-        uint8_t* vs = smem[stage][1];
+        if (does_k) {
+            uint8_t* ks = smem[stage];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int key = k_key0 + 16 * i;
-            const int phys = k_chunk ^ (key & 15);
-            *reinterpret_cast<u32x4_t*>(ks + key * 256 + phys * 16) = kreg[i];
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<u32x4_t*>(ks + (k_key0 + 16 * i) * kKPitch + k_chunk * 16) = kreg[i];
         }
-        // transpose 8 keys x 4 d into 4 rows of V^T (8 keys each)
+        if (does_v) {
+            uint8_t* vs = smem[stage] + kKBytes;
+            // transpose 8 keys x 4 d into 4 rows of V^T (8 keys each)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            u32x4_t o;
+            for (int j = 0; j < 4; ++j) {
+                u32x4_t o;
 #pragma unroll
-            for (int q2 = 0; q2 < 4; ++q2) {
-                const uint32_t a = (j < 2) ? vreg[2 * q2].x : vreg[2 * q2].y;
-                const uint32_t c = (j < 2) ? vreg[2 * q2 + 1].x : vreg[2 * q2 + 1].y;
-                o[q2] = (j & 1) ? pack_hi(a, c) : pack_lo(a, c);
+                for (int q2 = 0; q2 < 4; ++q2) {
+                    const uint32_t a = (j < 2) ? vreg[2 * q2].x : vreg[2 * q2].y;
+                    const uint32_t c = (j < 2) ? vreg[2 * q2 + 1].x : vreg[2 * q2 + 1].y;
+                    o[q2] = (j & 1) ? pack_hi(a, c) : pack_lo(a, c);
+                }
+                const int d = 4 * v_dg + j;
+                *reinterpret_cast<u32x4_t*>(vs + d * kVPitch + ((v_kg ^ ((d >> 1) & 7)) * 16)) = o;
             }
-            const int d = 4 * v_dg + j;
-            const int phys = v_kg ^ ((d >> 1) & 7);
-            *reinterpret_cast<u32x4_t*>(vs + d * 128 + phys * 16) = o;
         }
     };
 
     const float sl2 = p.scale_log2;
 
+    // One 64-key block: S^T = K Q^T (16 MFMAs), online softmax with lazy rescale, then
+    // O^T += V^T P^T (16 MFMAs).  m_run only rises when a row's scaled block max exceeds it
+    // by more than kRescale (log2 units); otherwise P = exp2(s - m_run) < 2^kRescale and the
+    // accumulators keep their scale.
+    // Fragment addresses: lane-constant bases, per-fragment offsets are immediates.
+    const int k_lane = swap23(n) * kKPitch + h * 16;
+    const int v_lane = n * kVPitch;
+    auto process = [&](int kb, const uint8_t* stage_base, bool masked) {
+        const uint8_t* ks = stage_base + k_lane;
+        const uint8_t* vs = stage_base + kKBytes + v_lane;
+        f32x16_t sacc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.0f;
+        // the two 32-key accumulators alternate so consecutive MFMAs are independent
+#pragma unroll
+        for (int ds = 0; ds < 8; ++ds)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt) {
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + kt * 32 * kKPitch + ds * 32);
+                sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ds], sacc[kt], 0, 0, 0);
+            }
+        if (masked) {
+            // value j of half kt holds key kt*32 + swap23(8*(j/4) + 4*h + j%4)
+            // = kt*32 + 8*h + key_off(j); visible iff kb*64 + key <= 64*P + t
+            const int vis = P * 64 + qtok - kb * 64 - 8 * h;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) {
+                    const int key = kt * 32 + 16 * (j >> 3) + 4 * ((j >> 2) & 1) + (j & 3);
+                    if (key > vis) sacc[kt][j] = -__builtin_inff();
+                }
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sacc[kt][j]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+        float alpha = 1.0f;
+        if (mx > m_run + kRescale) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when m_run = -inf
+            m_run = mx;
+            l_run *= alpha;
+        }
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
+        }
+        const float m_use = m_run == -__builtin_inff() ? 0.0f : m_run;
+        bf16x8_t pf[4];
+        float rs = 0.0f;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            f32x8_t pv8;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                pv8[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[s4 >> 1][8 * (s4 & 1) + i], sl2, -m_use));
+            pf[s4] = __builtin_convertvector(pv8, bf16x8_t);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) rs += pv8[i];
+        }
+        l_run += rs;  // this lane's half of the row; combined across lanes n, n+32 at the end
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(vs + dt * 32 * kVPitch + (((2 * s4 + h) ^ ((n >> 1) & 7)) * 16));
+                oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[s4], oacc[dt], 0, 0, 0);
+            }
+        }
+    };
+
+    // ---- KV loop: two LDS stages, next block's global loads in flight during compute ----
     if (e0 < e1) {
         load_block(e0);
         store_block(0);
         __syncthreads();
     }
-    for (int e = e0; e < e1; ++e) {
+    auto step = [&](int e, bool masked) {
         const int stage = (e - e0) & 1;
         const bool has_next = e + 1 < e1;
         if (has_next) load_block(e + 1);
-        const int kb = block_id(e);
-        const uint8_t* ks = smem[stage][0];
-        const uint8_t* vs = smem[stage][1];
-
-        // The 64-key block is processed as two 32-key halves, each one online-softmax step:
-        // S^T_half (32 keys x 64 rows) -> P -> O^T += V^T_half P^T_half.
-        const bool need_mask = kb * 64 + 63 > P * 64 + t_first;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-            // ---- S^T = K Q^T for keys kt*32 .. kt*32+31 ----
-            f32x16_t sacc[2];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) sacc[rt][j] = 0.0f;
-            const int kk = kt * 32 + swap23(n);
-#pragma unroll
-            for (int ds = 0; ds < 8; ++ds) {
-                const int phys = (2 * ds + h) ^ (kk & 15);
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + kk * 256 + phys * 16);
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
-                    sacc[rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[rt][ds], sacc[rt], 0, 0, 0);
-            }
-
-            // ---- online softmax (log2 domain, lazy rescale) ----
-            // m_run is only raised when a row's max exceeds it by more than kRescale (log2
-            // units); otherwise P = exp2(s - m_run) < 2^kRescale and O^T / l keep their scale,
-            // so the accumulators are rarely touched by VALU code.
-            float alpha[2];
-#pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-                // key kt*32 + swap23(8*(j/4) + 4*h + j%4) = kt*32 + 8*h + key_off(j) is visible
-                // iff its position kb*64 + key <= 64*P + t
-                const int vis = P * 64 + qtok[rt] - kb * 64 - kt * 32 - 8 * h;
-                float mx = -__builtin_inff();
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    float v = sacc[rt][j] * sl2;
-                    const int key_off = 16 * (j >> 3) + 4 * ((j >> 2) & 1) + (j & 3);
-                    if (need_mask && key_off > vis) v = -__builtin_inff();
-                    sacc[rt][j] = v;
-                    mx = fmaxf(mx, v);
-                }
-                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-                alpha[rt] = 1.0f;
-                if (mx > m_run[rt] + kRescale) {
-                    alpha[rt] = __builtin_amdgcn_exp2f(m_run[rt] - mx);  // 0 when m_run = -inf
-                    m_run[rt] = mx;
-                }
-                const float m_use = m_run[rt] == -__builtin_inff() ? 0.0f : m_run[rt];
-                float rs = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 16; ++j) {
-                    const float pv = __builtin_amdgcn_exp2f(sacc[rt][j] - m_use);
-                    sacc[rt][j] = pv;
-                    rs += pv;
-                }
-                rs += __shfl_xor(rs, 32, 64);
-                l_run[rt] = l_run[rt] * alpha[rt] + rs;
-            }
-            if (__ballot(alpha[0] != 1.0f || alpha[1] != 1.0f)) {
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-                    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                        for (int j = 0; j < 16; ++j) oacc[dt][rt][j] *= alpha[rt];
-            }
-
-            // ---- O^T += V^T P^T over the same 32 keys ----
-#pragma unroll
-            for (int sh = 0; sh < 2; ++sh) {
-                const int s4 = 2 * kt + sh;
-                bf16x8_t pf[2];
-#pragma unroll
-                for (int rt = 0; rt < 2; ++rt) {
-                    f32x8_t pv8;
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) pv8[i] = sacc[rt][8 * sh + i];
-                    pf[rt] = __builtin_convertvector(pv8, bf16x8_t);
-                }
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    const int d = dt * 32 + n;
-                    const int phys = (2 * s4 + h) ^ ((d >> 1) & 7);
-                    const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(vs + d * 128 + phys * 16);
-#pragma unroll
-                    for (int rt = 0; rt < 2; ++rt)
-                        oacc[dt][rt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[rt], oacc[dt][rt], 0, 0, 0);
-                }
-            }
-        }
-
+        process(block_id(e), smem[stage], masked);
         if (has_next) store_block(stage ^ 1);
         __syncthreads();
-    }
+    };
+    int e = e0;
+    for (; e < e_mask; ++e) step(e, false);
+    for (; e < e1; ++e) step(e, true);
+    (void)kt_id;
 
     // ---- epilogue ----
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        if (!qvalid[rt]) continue;
-        const int r = r0 + 64 * w + 32 * rt + n;
-        const float lsum = l_run[rt];
-        const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-        const float lse2 = lsum > 0.0f ? m_run[rt] + __log2f(lsum) : -__builtin_inff();
+    // lanes n and n + 32 hold different keys of the same row: their partial sums combine
+    // here (both were rescaled by the same factors)
+    l_run += __shfl_xor(l_run, 32, 64);
+    if (qvalid) {
+        const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+        const float lse2 = l_run > 0.0f ? m_run + __log2f(l_run) : -__builtin_inff();
         if (p.splits == 1) {
-            const int t = qtok[rt];
-            const int hq = hk * G + qg[rt];
-            uint16_t* op = p.out.data + b * p.out.sb + (int64_t)t * p.out.st + (int64_t)hq * p.out.sh;
+            const int hq = hk * G + qg;
+            uint16_t* op = p.out.data + b * p.out.sb + (int64_t)qt * p.out.st + (int64_t)hq * p.out.sh;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
@@ -333,12 +339,12 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
                     const int d0 = dt * 32 + 8 * jq + 4 * h;
                     f32x4_t o4;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) o4[i] = oacc[dt][rt][4 * jq + i] * inv;
+                    for (int i = 0; i < 4; ++i) o4[i] = oacc[dt][4 * jq + i] * inv;
                     *reinterpret_cast<bf16x4_t*>(op + d0) = __builtin_convertvector(o4, bf16x4_t);
                 }
-            if (p.lse && h == 0) p.lse[((int64_t)b * s.Hq + hq) * s.Lq + t] = lse2 * 0.69314718055994531f;
+            if (p.lse && h == 0) p.lse[((int64_t)b * s.Hq + hq) * s.Lq + qt] = lse2 * 0.69314718055994531f;
         } else {
-            const int64_t prow = ((int64_t)split * (s.B * s.Hkv) + row) * rows_total + r;
+            const int64_t prow = ((int64_t)split * (s.B * s.Hkv) + row) * rows_total + qrow;
             float* wo = p.ws_o + prow * 128;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
@@ -346,10 +352,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnParams p) {
                 for (int jq = 0; jq < 4; ++jq) {
                     const int d0 = dt * 32 + 8 * jq + 4 * h;
                     float4 o;
-                    o.x = oacc[dt][rt][4 * jq + 0] * inv;
-                    o.y = oacc[dt][rt][4 * jq + 1] * inv;
-                    o.z = oacc[dt][rt][4 * jq + 2] * inv;
-                    o.w = oacc[dt][rt][4 * jq + 3] * inv;
+                    o.x = oacc[dt][4 * jq + 0] * inv;
+                    o.y = oacc[dt][4 * jq + 1] * inv;
+                    o.z = oacc[dt][4 * jq + 2] * inv;
+                    o.w = oacc[dt][4 * jq + 3] * inv;
                     *reinterpret_cast<float4*>(wo + d0) = o;
                 }
             if (h == 0) p.ws_lse[prow] = lse2;
@@ -402,13 +408,18 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 }  // namespace
 
 int attn_pick_splits(const Shape& s, const PastBlocks& pb) {
+    // Two workgroups are resident per CU (70 KB LDS and <= 256 registers per lane each).  A
+    // launch wants about two rounds of them (4 x 256 workgroups) to even out the per-tile
+    // work differences, so the block lists are split when the work items alone do not reach
+    // that, keeping at least ~16 blocks per split.
     const int rows_total = s.Lq * s.G;
     const int ntiles = (rows_total + kBM - 1) / kBM;
     const int items = s.B * s.Hkv * ntiles;
+    constexpr int kSlots = 4 * 256;  // two resident rounds: smooths the per-tile work imbalance
     int max_blocks = 0;
     for (int b = 0; b < s.B; ++b) max_blocks = max(max_blocks, pb.p[b] + s.Qb);
-    int splits = (256 + items - 1) / items;  // fill the 256 CUs
-    const int by_work = max(1, max_blocks / 32);
+    int splits = items >= kSlots ? 1 : (kSlots + items / 2) / items;
+    const int by_work = max(1, max_blocks / 16);
     if (splits > by_work) splits = by_work;
     if (splits > 16) splits = 16;
     if (splits < 1) splits = 1;
@@ -442,7 +453,7 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     const int64_t rows_all = (int64_t)a.s.B * a.s.Hkv * p.rows_total;
     p.ws_o = a.num_splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
     p.ws_lse = a.num_splits > 1 ? p.ws_o + (int64_t)a.num_splits * rows_all * 128 : nullptr;
-    hipLaunchKernelGGL(attn_fwd_kernel, dim3(p.per_xcd * 8), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(attn_fwd_kernel<kNW>, dim3(p.per_xcd * 8), dim3(kNW * 64), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || a.num_splits <= 1) return e;
     const int64_t blocks = (rows_all + 7) / 8;

@@ -46,6 +46,8 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
                                int64_t ssq, const ca_select_rule& rule, const PastBlocks& pb,
                                uint32_t* rowmask, float* scores_out, hipStream_t stream);
 
+size_t union_lds_bytes(const Shape& s);
+
 hipError_t launch_union_compact(const Shape& s, const uint32_t* rowmask, int last_n_block,
                                 const uint8_t* keep_kv_in, const PastBlocks& pb, uint8_t* keep_block,
                                 uint8_t* keep_kv, int32_t* table, int64_t table_stride,

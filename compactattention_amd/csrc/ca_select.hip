@@ -56,106 +56,195 @@ __device__ void gate_project_rope(const float* xs, const float* w, const float* 
 }
 
 // ---------------------------------------------------------------------------------------
-// Cache fill: one 64-token block of one (request, KV head) per workgroup.  Threads 0..63 copy
-// K (two head-dim lanes each) and accumulate the block mean; threads 64..127 copy V.
-__global__ __launch_bounds__(128) void cache_fill_kernel(Shape s, SeqAddr kn, SeqAddr vn,
+// Block staging shared by cache fill and query pooling: 256 threads move one 64-token x 128
+// block with 16-byte accesses (thread t: token t/16 + 16 i, 8-element chunk t%16) and keep
+// a bf16 copy in LDS; the block mean is then a sequential sum over the 64 tokens per head
+// dim (threads 0..127), times 1/64.
+constexpr int kTilePitch = kD + 8;  // bf16 elements per staged token row
+
+__device__ __forceinline__ float block_mean_from_lds(const uint16_t* tile, int d) {
+    float sum = 0.0f;
+#pragma unroll 16
+    for (int t = 0; t < kBlock; ++t) sum = sum + bf16_to_f32(tile[t * kTilePitch + d]);
+    return sum * 0.015625f;
+}
+
+typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
+
+// Cache fill: one (new block, request x KV head) per workgroup.
+__global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, SeqAddr vn,
                                                          KvAddr kc, KvAddr vc, PastBlocks pb,
                                                          float* kmean, const float* wk,
                                                          const float* rope_cos,
                                                          const float* rope_sin, float* kgate) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
+    __shared__ float xs[kD];
     const int j = blockIdx.x;
     const int row = blockIdx.y;
     const int b = row / s.Hkv;
     const int hk = row - b * s.Hkv;
     const int kb = pb.p[b] + j;
-    const bool is_v = threadIdx.x >= 64;
-    const int lane = threadIdx.x & 63;
-    const SeqAddr& src = is_v ? vn : kn;
-    const KvAddr& dst = is_v ? vc : kc;
-    const int64_t phys = dst.page_table ? dst.page_table[(int64_t)row * dst.pts + kb] : kb;
-    const uint16_t* sp = src.data + b * src.sb + (int64_t)j * kBlock * src.st + hk * src.sh + 2 * lane;
-    uint16_t* dp = dst.data + b * dst.sb + hk * dst.sh + phys * dst.sblk + 2 * lane;
-    float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll 8
-    for (int t = 0; t < kBlock; ++t) {
-        const uint32_t v = *reinterpret_cast<const uint32_t*>(sp + t * src.st);
-        *reinterpret_cast<uint32_t*>(dp + t * dst.stok) = v;
-        s0 = s0 + bf16_to_f32(static_cast<uint16_t>(v & 0xffffu));
-        s1 = s1 + bf16_to_f32(static_cast<uint16_t>(v >> 16));
+    const int t = threadIdx.x;
+    const int tok0 = t >> 4;
+    const int ch = t & 15;
+    const int64_t kphys = kc.page_table ? kc.page_table[(int64_t)row * kc.pts + kb] : kb;
+    const int64_t vphys = vc.page_table ? vc.page_table[(int64_t)row * vc.pts + kb] : kb;
+    const uint16_t* ks = kn.data + b * kn.sb + (int64_t)j * kBlock * kn.st + hk * kn.sh + 8 * ch;
+    const uint16_t* vsrc = vn.data + b * vn.sb + (int64_t)j * kBlock * vn.st + hk * vn.sh + 8 * ch;
+    uint16_t* kd = kc.data + b * kc.sb + hk * kc.sh + kphys * kc.sblk + 8 * ch;
+    uint16_t* vd = vc.data + b * vc.sb + hk * vc.sh + vphys * vc.sblk + 8 * ch;
+    u32x4_v kr[4], vr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + 16 * i;
+        kr[i] = *reinterpret_cast<const u32x4_v*>(ks + (int64_t)tok * kn.st);
+        vr[i] = *reinterpret_cast<const u32x4_v*>(vsrc + (int64_t)tok * vn.st);
     }
-    __shared__ float xs[kD];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + 16 * i;
+        *reinterpret_cast<u32x4_v*>(kd + (int64_t)tok * kc.stok) = kr[i];
+        *reinterpret_cast<u32x4_v*>(vd + (int64_t)tok * vc.stok) = vr[i];
+        *reinterpret_cast<u32x4_v*>(tile + tok * kTilePitch + 8 * ch) = kr[i];
+    }
+    if (kmean == nullptr && wk == nullptr) return;
+    __syncthreads();
     const int64_t srow = ((int64_t)row * s.cap + kb) * kD;
-    if (!is_v) {
-        const float m0 = s0 * 0.015625f;
-        const float m1 = s1 * 0.015625f;
-        if (kmean) {
-            kmean[srow + 2 * lane] = m0;
-            kmean[srow + 2 * lane + 1] = m1;
-        }
-        xs[2 * lane] = m0;
-        xs[2 * lane + 1] = m1;
+    if (t < kD) {
+        const float m = block_mean_from_lds(tile, t);
+        if (kmean) kmean[srow + t] = m;
+        xs[t] = m;
     }
     if (wk == nullptr) return;
     __syncthreads();
-    if (!is_v) gate_project_rope(xs, wk + (int64_t)hk * kD * kD, rope_cos, rope_sin, kb, kgate + srow);
+    if (t < 64) gate_project_rope(xs, wk + (int64_t)hk * kD * kD, rope_cos, rope_sin, kb, kgate + srow);
 }
 
 // ---------------------------------------------------------------------------------------
-// Query-block means (optionally gate-projected and rotated): one (block, request, head) per
-// workgroup of 64 threads, two head-dim lanes per thread.
-__global__ __launch_bounds__(64) void pool_query_kernel(Shape s, SeqAddr q, PastBlocks pb,
-                                                        const float* wq, const float* rope_cos,
-                                                        const float* rope_sin, float* qhat) {
+// Query-block means (optionally gate-projected and rotated): one (block, request x head)
+// per workgroup.
+__global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, PastBlocks pb,
+                                                         const float* wq, const float* rope_cos,
+                                                         const float* rope_sin, float* qhat) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
+    __shared__ float xs[kD];
     const int qb = blockIdx.x;
     const int bh = blockIdx.y;
     const int b = bh / s.Hq;
     const int h = bh - b * s.Hq;
-    const int lane = threadIdx.x;
-    const uint16_t* sp = q.data + b * q.sb + (int64_t)qb * kBlock * q.st + h * q.sh + 2 * lane;
-    float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll 8
-    for (int t = 0; t < kBlock; ++t) {
-        const uint32_t v = *reinterpret_cast<const uint32_t*>(sp + t * q.st);
-        s0 = s0 + bf16_to_f32(static_cast<uint16_t>(v & 0xffffu));
-        s1 = s1 + bf16_to_f32(static_cast<uint16_t>(v >> 16));
+    const int t = threadIdx.x;
+    const int tok0 = t >> 4;
+    const int ch = t & 15;
+    const uint16_t* sp = q.data + b * q.sb + (int64_t)qb * kBlock * q.st + h * q.sh + 8 * ch;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int tok = tok0 + 16 * i;
+        *reinterpret_cast<u32x4_v*>(tile + tok * kTilePitch + 8 * ch) =
+            *reinterpret_cast<const u32x4_v*>(sp + (int64_t)tok * q.st);
     }
-    float* out = qhat + ((int64_t)bh * s.Qb + qb) * kD;
-    const float m0 = s0 * 0.015625f;
-    const float m1 = s1 * 0.015625f;
-    if (wq == nullptr) {
-        out[2 * lane] = m0;
-        out[2 * lane + 1] = m1;
-        return;
-    }
-    __shared__ float xs[kD];
-    xs[2 * lane] = m0;
-    xs[2 * lane + 1] = m1;
     __syncthreads();
-    gate_project_rope(xs, wq + (int64_t)h * kD * kD, rope_cos, rope_sin, (int64_t)pb.p[b] + qb, out);
+    float* out = qhat + ((int64_t)bh * s.Qb + qb) * kD;
+    if (t < kD) {
+        const float m = block_mean_from_lds(tile, t);
+        if (wq == nullptr)
+            out[t] = m;
+        else
+            xs[t] = m;
+    }
+    if (wq == nullptr) return;
+    __syncthreads();
+    if (t < 64) gate_project_rope(xs, wq + (int64_t)h * kD * kD, rope_cos, rope_sin, (int64_t)pb.p[b] + qb, out);
 }
 
 // ---------------------------------------------------------------------------------------
-// Scoring + selection.  One workgroup (256 threads) per (request, KV head, query block)
-// handles the G rows of the group's Q heads.
+// Block logits: logits[(b*Hq + h)*Qb + qb][kb] = dot(qhat[b,h,qb], khat[b, h/G, kb]) * scale
+// for the causal kb <= P + qb.  The G*Qb query vectors of a KV group are contiguous in
+// qhat, so a workgroup takes a 64 (query vectors) x 64 (key blocks) tile of one group;
+// each thread owns a 4 x 4 register tile and every dot product is one sequential fma chain
+// over d = 0..127.
 constexpr int kPadRow = kD + 4;  // LDS row pitch (floats) for summary tiles
 
-__device__ __forceinline__ int score_tile_rows(int G) {
-    const int r = 256 / G;
-    return r < 64 ? r : 64;
+__global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float* qhat, const float* khat,
+                                                           float scale, PastBlocks pb, float* logits) {
+    __shared__ __attribute__((aligned(16))) float qt[64 * kPadRow];
+    __shared__ __attribute__((aligned(16))) float kt[64 * kPadRow];
+    const int kb0 = blockIdx.x * 64;
+    const int row = blockIdx.y;
+    const int m0 = blockIdx.z * 64;
+    const int b = row / s.Hkv;
+    const int hk = row - b * s.Hkv;
+    const int P = pb.p[b];
+    const int nkb = P + s.Qb;
+    const int M = s.G * s.Qb;
+    if (kb0 >= nkb || m0 >= M) return;
+    const int t = threadIdx.x;
+    const float* qbase = qhat + ((int64_t)(b * s.Hq + hk * s.G) * s.Qb + m0) * kD;
+    const float* kbase = khat + ((int64_t)row * s.cap + kb0) * kD;
+    const int mrows = min(64, M - m0);
+    const int krows = min(64, nkb - kb0);
+    for (int f = t; f < 64 * (kD / 4); f += 256) {
+        const int r = f >> 5, c4 = f & 31;
+        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r < mrows) qv = *reinterpret_cast<const float4*>(qbase + (int64_t)r * kD + c4 * 4);
+        if (r < krows) kv = *reinterpret_cast<const float4*>(kbase + (int64_t)r * kD + c4 * 4);
+        *reinterpret_cast<float4*>(qt + r * kPadRow + c4 * 4) = qv;
+        *reinterpret_cast<float4*>(kt + r * kPadRow + c4 * 4) = kv;
+    }
+    __syncthreads();
+    const int lane = t & 63;
+    const int tm = lane & 15;              // query rows tm + 16 i
+    const int tn = (t >> 6) * 4 + (lane >> 4);  // key rows 4 tn + j
+    float acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+    for (int d = 0; d < kD; d += 4) {
+        float4 a[4], c[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(qt + (tm + 16 * i) * kPadRow + d);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = *reinterpret_cast<const float4*>(kt + (4 * tn + j) * kPadRow + d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float v = acc[i][j];
+                v = __builtin_fmaf(a[i].x, c[j].x, v);
+                v = __builtin_fmaf(a[i].y, c[j].y, v);
+                v = __builtin_fmaf(a[i].z, c[j].z, v);
+                v = __builtin_fmaf(a[i].w, c[j].w, v);
+                acc[i][j] = v;
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + tm + 16 * i;
+        if (m >= M) continue;
+        const int qb = m % s.Qb;
+        float* out = logits + ((int64_t)(b * s.Hq + hk * s.G) * s.Qb + m) * s.cap;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int kb = kb0 + 4 * tn + j;
+            if (kb <= P + qb) out[kb] = acc[i][j] * scale;
+        }
+    }
 }
 
+// ---------------------------------------------------------------------------------------
+// Row softmax + selection: one wavefront (workgroup of 64) per (b, h, qb) row, no block
+// barriers beyond the single wave's.  Softmax sum order: lane l sums kb = l, l+64, ...
+// ascending, then the tree part[l] += part[l+s], s = 32..1.
 struct SelectParams {
     Shape s;
-    const float* qhat;
-    const float* khat;
-    float scale;
-    const void* scores_in;
+    float* scores;          // [B*Hq*Qb][cap]: logits in, probabilities out (compute mode)
+    const void* scores_in;  // caller scores (select mode)
     int dtype;
     int64_t ssb, ssh, ssq;
     ca_select_rule rule;
     PastBlocks pb;
     uint32_t* rowmask;
-    float* scores_out;
 };
 
 // Monotone uint32 key of a float (larger float -> larger key); -0 is folded onto +0.
@@ -169,188 +258,175 @@ __device__ __forceinline__ bool is_finite_f(float v) {
     return (__float_as_uint(v) & 0x7f800000u) != 0x7f800000u;
 }
 
-template <bool kCompute>
-__global__ __launch_bounds__(256) void score_select_kernel(SelectParams p) {
-    extern __shared__ float lds[];
-    __shared__ float red[256];
-    __shared__ int ired[8];
-    __shared__ int hist[256];
-    __shared__ int sel_digit, sel_above;
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
 
+__device__ __forceinline__ int wave_sum_int(int v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int y = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += y;
+    }
+    return incl - v;
+}
+
+template <bool kCompute>
+__global__ __launch_bounds__(64) void row_select_kernel(SelectParams p) {
+    extern __shared__ float row[];  // [cap]
+    __shared__ int hist[256];
     const Shape& s = p.s;
-    const int qb = blockIdx.x;
-    const int row = blockIdx.y;
-    const int b = row / s.Hkv;
-    const int hk = row - b * s.Hkv;
-    const int G = s.G;
-    const int t = threadIdx.x;
+    const int rid = blockIdx.x;  // (b*Hq + h)*Qb + qb
+    const int qb = rid % s.Qb;
+    const int bh = rid / s.Qb;
+    const int b = bh / s.Hq;
+    const int h = bh - b * s.Hq;
+    const int lane = threadIdx.x;
     const int P = p.pb.p[b];
     const int qabs = P + qb;
-    const int n = qabs + 1;  // causal columns
+    const int n = qabs + 1;
     const int cap = s.cap;
-    float* sc = lds;  // [G][cap]
 
     if (kCompute) {
-        float* qv = lds + (size_t)G * cap;  // [G][kPadRow]
-        float* kt = qv + (size_t)G * kPadRow;  // [TK][kPadRow]
-        const int TK = score_tile_rows(G);
-        for (int i = t; i < G * kD; i += 256) {
-            const int g = i / kD, d = i - g * kD;
-            qv[g * kPadRow + d] =
-                p.qhat[(((int64_t)b * s.Hq + hk * G + g) * s.Qb + qb) * kD + d];
+        float* srow = p.scores + (int64_t)rid * cap;
+        float m = -__builtin_inff();
+        for (int kb = lane; kb < n; kb += 64) {
+            const float v = srow[kb];
+            row[kb] = v;
+            m = fmaxf(m, v);
         }
-        const float* kbase = p.khat + (int64_t)row * cap * kD;
-        for (int kb0 = 0; kb0 < n; kb0 += TK) {
-            const int rows_here = min(TK, n - kb0);
-            __syncthreads();
-            for (int f = t; f < rows_here * (kD / 4); f += 256) {
-                const int r = f >> 5, c4 = f & 31;
-                const float4 v = *reinterpret_cast<const float4*>(kbase + (int64_t)(kb0 + r) * kD + c4 * 4);
-                *reinterpret_cast<float4*>(kt + r * kPadRow + c4 * 4) = v;
-            }
-            __syncthreads();
-            if (t < TK * G) {
-                const int kl = t / G, g = t - kl * G;
-                if (kl < rows_here) {
-                    const float* a = qv + g * kPadRow;
-                    const float* k = kt + kl * kPadRow;
-                    float acc = 0.0f;
-#pragma unroll 16
-                    for (int d = 0; d < kD; ++d) acc = __builtin_fmaf(a[d], k[d], acc);
-                    sc[g * cap + kb0 + kl] = acc * p.scale;
-                }
-            }
+        m = wave_max(m);
+        float part = 0.0f;
+        for (int kb = lane; kb < n; kb += 64) {
+            const float e = exp_fixed(row[kb] - m);
+            row[kb] = e;
+            part = part + e;
         }
-        __syncthreads();
-        // softmax over the causal columns of each row
-        for (int g = 0; g < G; ++g) {
-            float* r = sc + g * cap;
-            float m = -__builtin_inff();
-            for (int kb = t; kb < n; kb += 256) m = fmaxf(m, r[kb]);
-            m = block_max256(m, red);
-            float part = 0.0f;
-            for (int kb = t; kb < n; kb += 256) {
-                const float e = exp_fixed(r[kb] - m);
-                r[kb] = e;
-                part = part + e;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) part = part + __shfl_down(part, o, 64);
+        const float sum = __shfl(part, 0, 64);
+        for (int kb = lane; kb < cap; kb += 64) {
+            float v = 0.0f;
+            if (kb < n) {
+                v = row[kb] / sum;
+                row[kb] = v;
             }
-            const float sum = tree256_sum(part, red);
-            for (int kb = t; kb < n; kb += 256) r[kb] = r[kb] / sum;
-            if (p.scores_out) {
-                float* o = p.scores_out + (((int64_t)b * s.Hq + hk * G + g) * s.Qb + qb) * cap;
-                for (int kb = t; kb < cap; kb += 256) o[kb] = kb < n ? r[kb] : 0.0f;
-            }
+            srow[kb] = v;
         }
-        __syncthreads();
     } else {
-        for (int g = 0; g < G; ++g) {
-            const int h = hk * G + g;
-            const int64_t off = b * p.ssb + h * p.ssh + qb * p.ssq;
-            for (int kb = t; kb < n; kb += 256) {
-                float v;
-                if (p.dtype == 0)
-                    v = static_cast<const float*>(p.scores_in)[off + kb];
-                else
-                    v = bf16_to_f32(static_cast<const uint16_t*>(p.scores_in)[off + kb]);
-                sc[g * cap + kb] = v;
-            }
+        const int64_t off = b * p.ssb + h * p.ssh + qb * p.ssq;
+        for (int kb = lane; kb < n; kb += 64) {
+            float v;
+            if (p.dtype == 0)
+                v = static_cast<const float*>(p.scores_in)[off + kb];
+            else
+                v = bf16_to_f32(static_cast<const uint16_t*>(p.scores_in)[off + kb]);
+            row[kb] = v;
         }
-        __syncthreads();
     }
+    __syncthreads();
 
-    // ---- selection, one row at a time ----
     const ca_select_rule& rule = p.rule;
     const bool use_topk = (rule.flags & CA_RULE_TOPK) && rule.topk > 0 && P > 0;
-    const int chunks = (s.words * 32 + 255) / 256;
-    const int wave = t >> 6, lane = t & 63;
-    for (int g = 0; g < G; ++g) {
-        const float* r = sc + g * cap;
-        float mx = 0.0f;
-        for (int kb = t; kb < n; kb += 256) {
-            const float v = r[kb];
-            if (is_finite_f(v)) mx = fmaxf(mx, v);
-        }
-        const float rowmax = block_max256(mx, red);
-        const float alpha_cut = rule.alpha * rowmax;
+    float mx = 0.0f;
+    for (int kb = lane; kb < n; kb += 64) {
+        const float v = row[kb];
+        if (is_finite_f(v)) mx = fmaxf(mx, v);
+    }
+    const float rowmax = wave_max(mx);
+    const float alpha_cut = rule.alpha * rowmax;
 
-        // top-k threshold key T and the number of ties at T to take (lowest ids first)
-        bool take_all = false;
-        uint32_t T = 0;
-        int krem = 0;
-        if (use_topk) {
-            int nc = 0;
-            for (int kb = t; kb < P; kb += 256) nc += is_finite_f(r[kb]) ? 1 : 0;
-            nc = block_sum256_int(nc, ired);
-            if (rule.topk >= nc) {
-                take_all = true;
-            } else {
-                uint32_t prefix = 0, pmask = 0;
-                krem = rule.topk;
-                for (int shift = 24; shift >= 0; shift -= 8) {
-                    hist[t] = 0;
-                    __syncthreads();
-                    for (int kb = t; kb < P; kb += 256) {
-                        const float v = r[kb];
-                        if (!is_finite_f(v)) continue;
-                        const uint32_t key = order_key(v);
-                        if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-                    }
-                    __syncthreads();
-                    // suffix counts from the top digit down: thread t looks at digit 255 - t
-                    const int hcount = hist[255 - t];
-                    int tot;
-                    const int excl = block_exclusive_scan256(hcount, ired, &tot);
-                    if (hcount > 0 && excl < krem && krem <= excl + hcount) {
-                        sel_digit = 255 - t;
-                        sel_above = excl;
-                    }
-                    __syncthreads();
-                    prefix |= static_cast<uint32_t>(sel_digit) << shift;
-                    pmask |= 255u << shift;
-                    krem -= sel_above;
-                    __syncthreads();
+    bool take_all = false;
+    uint32_t T = 0;
+    int krem = 0;
+    if (use_topk) {
+        int nc = 0;
+        for (int kb = lane; kb < P; kb += 64) nc += is_finite_f(row[kb]) ? 1 : 0;
+        nc = wave_sum_int(nc);
+        if (rule.topk >= nc) {
+            take_all = true;
+        } else {
+            uint32_t prefix = 0, pmask = 0;
+            krem = rule.topk;
+            for (int shift = 24; shift >= 0; shift -= 8) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) hist[lane + 64 * i] = 0;
+                __syncthreads();
+                for (int kb = lane; kb < P; kb += 64) {
+                    const float v = row[kb];
+                    if (!is_finite_f(v)) continue;
+                    const uint32_t key = order_key(v);
+                    if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
                 }
-                T = prefix;
+                __syncthreads();
+                // lane l owns digits 255-4l, 254-4l, 253-4l, 252-4l (descending)
+                int c[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) c[i] = hist[255 - 4 * lane - i];
+                const int excl = wave_excl_scan(c[0] + c[1] + c[2] + c[3], lane);
+                int run = excl, found = -1, above = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    if (found < 0 && c[i] > 0 && run < krem && krem <= run + c[i]) {
+                        found = 255 - 4 * lane - i;
+                        above = run;
+                    }
+                    run += c[i];
+                }
+                const uint64_t who = __ballot(found >= 0);
+                const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;
+                const int digit = __shfl(found, src, 64);
+                const int abv = __shfl(above, src, 64);
+                prefix |= static_cast<uint32_t>(digit) << shift;
+                pmask |= 255u << shift;
+                krem -= abv;
+                __syncthreads();
             }
+            T = prefix;
         }
+    }
 
-        const int h = hk * G + g;
-        uint32_t* out = p.rowmask + (((int64_t)b * s.Hq + h) * s.Qb + qb) * s.words;
-        int eq_base = 0;
-        for (int c = 0; c < chunks; ++c) {
-            const int kb = c * 256 + t;
-            bool keep = false;
-            bool eq = false;
-            if (kb < n) {
-                const float v = r[kb];
-                const bool fin = is_finite_f(v);
-                if ((rule.flags & CA_RULE_ALPHA) && fin && v >= alpha_cut) keep = true;
-                if ((rule.flags & CA_RULE_THRESHOLD) && v > rule.threshold) keep = true;
-                if (kb < rule.sink_blocks) keep = true;
-                if (qabs - kb < rule.window_blocks) keep = true;
-                if (kb < P && kb >= P - rule.local_blocks) keep = true;
-                if (use_topk && kb < P && fin) {
-                    if (take_all) {
-                        keep = true;
-                    } else {
-                        const uint32_t key = order_key(v);
-                        if (key > T) keep = true;
-                        eq = key == T;
-                    }
+    uint32_t* out = p.rowmask + (int64_t)rid * s.words;
+    const int chunks = (s.words + 1) / 2;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    int eq_base = 0;
+    for (int c = 0; c < chunks; ++c) {
+        const int kb = c * 64 + lane;
+        bool keep = false;
+        bool eq = false;
+        if (kb < n) {
+            const float v = row[kb];
+            const bool fin = is_finite_f(v);
+            if ((rule.flags & CA_RULE_ALPHA) && fin && v >= alpha_cut) keep = true;
+            if ((rule.flags & CA_RULE_THRESHOLD) && v > rule.threshold) keep = true;
+            if (kb < rule.sink_blocks) keep = true;
+            if (qabs - kb < rule.window_blocks) keep = true;
+            if (kb < P && kb >= P - rule.local_blocks) keep = true;
+            if (use_topk && kb < P && fin) {
+                if (take_all) {
+                    keep = true;
+                } else {
+                    const uint32_t key = order_key(v);
+                    if (key > T) keep = true;
+                    eq = key == T;
                 }
             }
-            if (use_topk && !take_all) {
-                int tot;
-                const int rank = block_exclusive_scan256(eq ? 1 : 0, ired, &tot);
-                if (eq && eq_base + rank < krem) keep = true;
-                eq_base += tot;
-            }
-            const uint64_t bal = __ballot(keep);
-            const int w0 = (c * 256 + wave * 64) >> 5;
-            if (lane == 0 && w0 < s.words) out[w0] = static_cast<uint32_t>(bal);
-            if (lane == 1 && w0 + 1 < s.words) out[w0 + 1] = static_cast<uint32_t>(bal >> 32);
         }
-        __syncthreads();
+        const uint64_t eqb = __ballot(eq);
+        if (eq && eq_base + __popcll(eqb & lt_mask) < krem) keep = true;
+        eq_base += __popcll(eqb);
+        const uint64_t bal = __ballot(keep);
+        if (lane == 0) out[2 * c] = static_cast<uint32_t>(bal);
+        if (lane == 1 && 2 * c + 1 < s.words) out[2 * c + 1] = static_cast<uint32_t>(bal >> 32);
     }
 }
 
@@ -381,7 +457,7 @@ __device__ __forceinline__ uint32_t range_bits(int w, int lo, int hi) {
 }
 
 __global__ __launch_bounds__(256) void union_compact_kernel(UnionParams p) {
-    extern __shared__ uint32_t kvw[];
+    extern __shared__ uint32_t lds_words[];  // [G][words] per-head union, then [words] KV union
     __shared__ int ired[8];
     const Shape& s = p.s;
     const int row = blockIdx.x;
@@ -391,22 +467,37 @@ __global__ __launch_bounds__(256) void union_compact_kernel(UnionParams p) {
     const int P = p.pb.p[b];
     const int nkb = P + s.Qb;
     const int G = s.G;
-    for (int w = t; w < s.words; w += 256) {
+    const int W = s.words;
+    uint32_t* hw = lds_words;           // [G][W]
+    uint32_t* kvw = lds_words + G * W;  // [W]
+    if (p.mode == 0) {
+        for (int i = t; i < G * W; i += 256) hw[i] = 0u;
+        __syncthreads();
+        // every (head, query block, word) of the group's row masks, OR-ed into LDS
+        const uint32_t* rm = p.rowmask + (int64_t)(b * s.Hq + hk * G) * s.Qb * W;
+        const int per_g = p.pooled * W;
+        for (int i = t; i < G * per_g; i += 256) {
+            const int g = i / per_g;
+            const int r = i - g * per_g;
+            const int qb = r / W;
+            const int w = r - qb * W;
+            const uint32_t v = rm[((int64_t)g * s.Qb + qb) * W + w];
+            if (v) atomicOr(&hw[g * W + w], v);
+        }
+        __syncthreads();
+    }
+    for (int w = t; w < W; w += 256) {
         const uint32_t valid = range_bits(w, 0, nkb);
         const uint32_t cur = range_bits(w, P, nkb);
         uint32_t acc = 0;
         if (p.mode == 0) {
             for (int g = 0; g < G; ++g) {
-                const int h = hk * G + g;
-                uint32_t hw = cur;
-                const uint32_t* rm = p.rowmask + ((int64_t)b * s.Hq + h) * s.Qb * s.words + w;
-                for (int qb = 0; qb < p.pooled; ++qb) hw |= rm[(int64_t)qb * s.words];
-                hw &= valid;
+                const uint32_t x = (hw[g * W + w] | cur) & valid;
                 if (p.keep_block) {
-                    uint8_t* kbk = p.keep_block + ((int64_t)b * s.Hq + h) * s.cap + 32 * w;
-                    for (int i = 0; i < 32 && 32 * w + i < s.cap; ++i) kbk[i] = (hw >> i) & 1u;
+                    uint8_t* kbk = p.keep_block + ((int64_t)b * s.Hq + hk * G + g) * s.cap + 32 * w;
+                    for (int i = 0; i < 32 && 32 * w + i < s.cap; ++i) kbk[i] = (x >> i) & 1u;
                 }
-                acc |= hw;
+                acc |= x;
             }
         } else if (p.mode == 1) {
             const uint8_t* src = p.keep_kv_in + (int64_t)row * s.cap + 32 * w;
@@ -422,9 +513,9 @@ __global__ __launch_bounds__(256) void union_compact_kernel(UnionParams p) {
         kvw[w] = acc;
     }
     __syncthreads();
-    const int wpt = (s.words + 255) / 256;
+    const int wpt = (W + 255) / 256;
     const int w0 = t * wpt;
-    const int w1 = min(w0 + wpt, s.words);
+    const int w1 = min(w0 + wpt, W);
     int cnt = 0;
     for (int w = w0; w < w1; ++w) cnt += __popc(kvw[w]);
     int total;
@@ -449,7 +540,7 @@ hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr
                              float* kmean, const float* wk, const float* rope_cos,
                              const float* rope_sin, float* kgate, hipStream_t stream) {
     dim3 grid(s.Qb, s.B * s.Hkv);
-    hipLaunchKernelGGL(cache_fill_kernel, grid, dim3(128), 0, stream, s, k_new, v_new, k_cache,
+    hipLaunchKernelGGL(cache_fill_kernel, grid, dim3(256), 0, stream, s, k_new, v_new, k_cache,
                        v_cache, pb, kmean, wk, rope_cos, rope_sin, kgate);
     return hipGetLastError();
 }
@@ -458,29 +549,32 @@ hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks&
                              const float* rope_cos, const float* rope_sin, float* qhat,
                              hipStream_t stream) {
     dim3 grid(s.Qb, s.B * s.Hq);
-    hipLaunchKernelGGL(pool_query_kernel, grid, dim3(64), 0, stream, s, q, pb, wq, rope_cos,
+    hipLaunchKernelGGL(pool_query_kernel, grid, dim3(256), 0, stream, s, q, pb, wq, rope_cos,
                        rope_sin, qhat);
     return hipGetLastError();
 }
 
 size_t score_select_lds_bytes(const Shape& s, bool compute) {
-    size_t bytes = sizeof(float) * (size_t)s.G * s.cap;
-    if (compute) {
-        const int tk = (256 / s.G) < 64 ? 256 / s.G : 64;
-        bytes += sizeof(float) * (size_t)(s.G + tk) * kPadRow;
-    }
-    return bytes;
+    (void)compute;
+    return sizeof(float) * (size_t)s.cap;
 }
 
 hipError_t launch_score_select(const Shape& s, const float* qhat, const float* khat, float scale,
                                const void* scores_in, int dtype, int64_t ssb, int64_t ssh,
                                int64_t ssq, const ca_select_rule& rule, const PastBlocks& pb,
-                               uint32_t* rowmask, float* scores_out, hipStream_t stream) {
+                               uint32_t* rowmask, float* scores, hipStream_t stream) {
+    const bool compute = scores_in == nullptr;
+    if (compute) {
+        int max_nkb = 0;
+        for (int b = 0; b < s.B; ++b) max_nkb = max(max_nkb, pb.p[b] + s.Qb);
+        dim3 grid((max_nkb + 63) / 64, s.B * s.Hkv, (s.G * s.Qb + 63) / 64);
+        hipLaunchKernelGGL(block_logits_kernel, grid, dim3(256), 0, stream, s, qhat, khat, scale, pb, scores);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     SelectParams p;
     p.s = s;
-    p.qhat = qhat;
-    p.khat = khat;
-    p.scale = scale;
+    p.scores = scores;
     p.scores_in = scores_in;
     p.dtype = dtype;
     p.ssb = ssb;
@@ -489,23 +583,16 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
     p.rule = rule;
     p.pb = pb;
     p.rowmask = rowmask;
-    p.scores_out = scores_out;
-    const bool compute = scores_in == nullptr;
     const size_t lds = score_select_lds_bytes(s, compute);
-    dim3 grid(s.Qb, s.B * s.Hkv);
-    if (compute) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(score_select_kernel<true>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(score_select_kernel<true>, grid, dim3(256), lds, stream, p);
-    } else {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(score_select_kernel<false>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        hipLaunchKernelGGL(score_select_kernel<false>, grid, dim3(256), lds, stream, p);
-    }
+    dim3 grid(s.B * s.Hq * s.Qb);
+    if (compute)
+        hipLaunchKernelGGL(row_select_kernel<true>, grid, dim3(64), lds, stream, p);
+    else
+        hipLaunchKernelGGL(row_select_kernel<false>, grid, dim3(64), lds, stream, p);
     return hipGetLastError();
 }
+
+size_t union_lds_bytes(const Shape& s) { return sizeof(uint32_t) * (size_t)(s.G + 1) * s.words; }
 
 hipError_t launch_union_compact(const Shape& s, const uint32_t* rowmask, int last_n_block,
                                 const uint8_t* keep_kv_in, const PastBlocks& pb, uint8_t* keep_block,
@@ -528,7 +615,7 @@ hipError_t launch_union_compact(const Shape& s, const uint32_t* rowmask, int las
     p.table = table;
     p.table_stride = table_stride;
     p.counts = counts;
-    const size_t lds = sizeof(uint32_t) * (size_t)s.words;
+    const size_t lds = union_lds_bytes(s);
     hipLaunchKernelGGL(union_compact_kernel, dim3(s.B * s.Hkv), dim3(256), lds, stream, p);
     return hipGetLastError();
 }

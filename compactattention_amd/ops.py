@@ -198,11 +198,11 @@ def score_select(qhat: torch.Tensor, khat: torch.Tensor, scale: float, rule: Rul
         raise ValueError("khat smaller than [B*Hkv, kv_cap, 128]")
     d = make_dims(B, Qb * BLOCK, Hq, num_kv_heads, kv_cap)
     rowmask = torch.empty((B, Hq, Qb, words_for(kv_cap)), dtype=torch.int32, device=qhat.device)
-    scores = torch.empty((B, Hq, Qb, kv_cap), dtype=torch.float32, device=qhat.device) if with_scores else None
+    scores = torch.empty((B, Hq, Qb, kv_cap), dtype=torch.float32, device=qhat.device)
     r = rule.to_c()
     check(_hip.lib().ca_score_select(ctypes.byref(d), qhat.data_ptr(), khat.data_ptr(), float(scale), ctypes.byref(r),
-                                     past_array(past_blocks), rowmask.data_ptr(), _ptr(scores), _stream()))
-    return rowmask, scores
+                                     past_array(past_blocks), rowmask.data_ptr(), scores.data_ptr(), _stream()))
+    return rowmask, (scores if with_scores else None)
 
 
 def select_scores(scores: torch.Tensor, rule: Rule, past_blocks: Sequence[int], num_kv_heads: int, kv_cap: int,

@@ -126,12 +126,13 @@ int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* pa
                   int64_t rope_rows, float* qhat, void* stream);
 
 /*
- * Fused block scoring and per-row selection.  For every (b, h, qb) row it computes
- * logits[kb] = dot(qhat[b,h,qb], khat[b, h/G, kb]) * scale for kb <= P_b + qb, the softmax
- * over those kb (fixed evaluation order), applies the rule and writes the row's keep
- * bitmask rowmask[((b*Hq + h)*Qb + qb)*words + w], words = ceil(kv_cap / 32), bit kb%32 of
- * word kb/32.  scores_out ([B, Hq, Qb, kv_cap] fp32, non-causal entries 0) is optional.
- * khat is a kmean/kgate summary array.
+ * Block scoring and per-row selection.  For every (b, h, qb) row it computes
+ * logits[kb] = dot(qhat[b,h,qb], khat[b, h/G, kb]) * scale for kb <= P_b + qb (sequential
+ * fma over d), the softmax over those kb (fixed evaluation order), applies the rule and
+ * writes the row's keep bitmask rowmask[((b*Hq + h)*Qb + qb)*words + w],
+ * words = ceil(kv_cap / 32), bit kb%32 of word kb/32.  scores ([B, Hq, Qb, kv_cap] fp32,
+ * required) receives the normalised scores (non-causal entries 0); it doubles as the
+ * logits scratch between the two kernels of this call.  khat is a kmean/kgate summary array.
  * Replaces: compute_block_score_chunked + normalize_scores (flashprefill_native_forward.py:
  * 98-207,365-374), AttnGate.score_compressed_blocks (attn_gate.py:173-204) and the per-row
  * rules of _flashprefill_keep_block_from_scores_rowwise (compact_attn/modules/
@@ -139,7 +140,7 @@ int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* pa
  */
 int ca_score_select(const ca_dims* dims, const float* qhat, const float* khat, float scale,
                     const ca_select_rule* rule, const int32_t* past_blocks_host, uint32_t* rowmask,
-                    float* scores_out, void* stream);
+                    float* scores, void* stream);
 
 /*
  * Per-row selection from caller-provided scores, element (b, h, qb, kb) at

@@ -137,18 +137,18 @@ void orc_gate_project(const float* x, int B, int H, int N, const float* W,
             }
 }
 
-/* Sum of e[0..n) in the kernels' order: 256 strided partial sums (partial t adds
- * e[t], e[t+256], ... in ascending order), then a halving tree part[t] += part[t+s]
- * for s = 128, 64, ..., 1. */
-static float tree256_sum(const float* e, int n) {
-    float part[256];
-    for (int t = 0; t < 256; ++t) {
+/* Sum of e[0..n) in the kernels' order: 64 strided partial sums (partial l adds
+ * e[l], e[l+64], ... in ascending order), then a halving tree part[l] += part[l+s]
+ * for s = 32, 16, ..., 1. */
+static float tree64_sum(const float* e, int n) {
+    float part[64];
+    for (int l = 0; l < 64; ++l) {
         float s = 0.0f;
-        for (int i = t; i < n; i += 256) s = s + e[i];
-        part[t] = s;
+        for (int i = l; i < n; i += 64) s = s + e[i];
+        part[l] = s;
     }
-    for (int s = 128; s >= 1; s >>= 1)
-        for (int t = 0; t < s; ++t) part[t] = part[t] + part[t + s];
+    for (int s = 32; s >= 1; s >>= 1)
+        for (int l = 0; l < s; ++l) part[l] = part[l] + part[l + s];
     return part[0];
 }
 
@@ -173,7 +173,7 @@ void orc_block_scores(const float* qhat, const float* khat, int B, int Hq, int H
                     if (logit[kb] > m) m = logit[kb];
                 }
                 for (int kb = 0; kb < n; ++kb) logit[kb] = orc_exp(logit[kb] - m);
-                const float sum = tree256_sum(logit, n);
+                const float sum = tree64_sum(logit, n);
                 for (int kb = 0; kb < cap; ++kb) srow[kb] = kb < n ? logit[kb] / sum : 0.0f;
             }
         }

@@ -241,8 +241,10 @@ def _attn_case(gpu, past_tokens, Lq, Hq, Hkv, layout, splits, keep_frac, seed):
     assert np.isfinite(got).all()
     assert err.max() <= ATOL_MAX, err.max()
     assert err.mean() <= ATOL_MEAN, err.mean()
+    # the kernel's row sums add the bf16-rounded probabilities the PV product uses, so its
+    # log-sum-exp carries the bf16 rounding of P (relative 2^-9 per term, averaging out)
     lerr = np.abs(f32(lse) - ref_lse)
-    assert lerr.max() <= 1e-3, lerr.max()
+    assert lerr.max() <= 4e-3, lerr.max()
 
 
 @pytest.mark.parametrize("splits", [1, 2, 3])
