@@ -149,12 +149,17 @@ int ca_cache_fill(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_
     ca::PastBlocks pb;
     int max_nkb = 0, rc;
     if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
-    ca::SeqAddr kn, vn;
-    ca::KvAddr kc, vc;
+    ca::SeqAddr kn{}, vn{};
+    ca::KvAddr kc{}, vc{};
     if ((rc = check_seq(k_new, "k_new", &kn)) != CA_OK) return rc;
-    if ((rc = check_seq(v_new, "v_new", &vn)) != CA_OK) return rc;
-    if ((rc = check_kv(k_cache, "k_cache", max_nkb, &kc)) != CA_OK) return rc;
-    if ((rc = check_kv(v_cache, "v_cache", max_nkb, &vc)) != CA_OK) return rc;
+    const bool copy = k_cache != nullptr || v_cache != nullptr;
+    if (copy) {
+        if ((rc = check_seq(v_new, "v_new", &vn)) != CA_OK) return rc;
+        if ((rc = check_kv(k_cache, "k_cache", max_nkb, &kc)) != CA_OK) return rc;
+        if ((rc = check_kv(v_cache, "v_cache", max_nkb, &vc)) != CA_OK) return rc;
+    } else if (kmean == nullptr && gate_wk == nullptr) {
+        return fail(CA_ERR_INVALID, "nothing to do: no cache and no summary output");
+    }
     if (kmean != nullptr && !aligned16(kmean)) return fail(CA_ERR_INVALID, "kmean misaligned");
     if (gate_wk != nullptr) {
         if (kgate == nullptr) return fail(CA_ERR_INVALID, "gate_wk given without kgate");

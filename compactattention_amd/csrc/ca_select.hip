@@ -87,26 +87,28 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
     const int t = threadIdx.x;
     const int tok0 = t >> 4;
     const int ch = t & 15;
-    const int64_t kphys = kc.page_table ? kc.page_table[(int64_t)row * kc.pts + kb] : kb;
-    const int64_t vphys = vc.page_table ? vc.page_table[(int64_t)row * vc.pts + kb] : kb;
     const uint16_t* ks = kn.data + b * kn.sb + (int64_t)j * kBlock * kn.st + hk * kn.sh + 8 * ch;
-    const uint16_t* vsrc = vn.data + b * vn.sb + (int64_t)j * kBlock * vn.st + hk * vn.sh + 8 * ch;
-    uint16_t* kd = kc.data + b * kc.sb + hk * kc.sh + kphys * kc.sblk + 8 * ch;
-    uint16_t* vd = vc.data + b * vc.sb + hk * vc.sh + vphys * vc.sblk + 8 * ch;
-    u32x4_v kr[4], vr[4];
+    u32x4_v kr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 16 * i;
-        kr[i] = *reinterpret_cast<const u32x4_v*>(ks + (int64_t)tok * kn.st);
-        vr[i] = *reinterpret_cast<const u32x4_v*>(vsrc + (int64_t)tok * vn.st);
+    for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const u32x4_v*>(ks + (int64_t)(tok0 + 16 * i) * kn.st);
+    if (kc.data != nullptr) {  // append K and V (summaries-only calls pass no cache)
+        const int64_t kphys = kc.page_table ? kc.page_table[(int64_t)row * kc.pts + kb] : kb;
+        const int64_t vphys = vc.page_table ? vc.page_table[(int64_t)row * vc.pts + kb] : kb;
+        const uint16_t* vsrc = vn.data + b * vn.sb + (int64_t)j * kBlock * vn.st + hk * vn.sh + 8 * ch;
+        uint16_t* kd = kc.data + b * kc.sb + hk * kc.sh + kphys * kc.sblk + 8 * ch;
+        uint16_t* vd = vc.data + b * vc.sb + hk * vc.sh + vphys * vc.sblk + 8 * ch;
+        u32x4_v vr[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) vr[i] = *reinterpret_cast<const u32x4_v*>(vsrc + (int64_t)(tok0 + 16 * i) * vn.st);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tok = tok0 + 16 * i;
+            *reinterpret_cast<u32x4_v*>(kd + (int64_t)tok * kc.stok) = kr[i];
+            *reinterpret_cast<u32x4_v*>(vd + (int64_t)tok * vc.stok) = vr[i];
+        }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 16 * i;
-        *reinterpret_cast<u32x4_v*>(kd + (int64_t)tok * kc.stok) = kr[i];
-        *reinterpret_cast<u32x4_v*>(vd + (int64_t)tok * vc.stok) = vr[i];
-        *reinterpret_cast<u32x4_v*>(tile + tok * kTilePitch + 8 * ch) = kr[i];
-    }
+    for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_v*>(tile + (tok0 + 16 * i) * kTilePitch + 8 * ch) = kr[i];
     if (kmean == nullptr && wk == nullptr) return;
     __syncthreads();
     const int64_t srow = ((int64_t)row * s.cap + kb) * kD;

@@ -129,15 +129,19 @@ class KV:
                                  page_table.stride(0)), page_table)
 
 
-def cache_fill(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV, v_cache: KV, past_blocks: Sequence[int],
-               kv_cap: int, kmean: Optional[torch.Tensor], gate_wk: Optional[torch.Tensor] = None,
-               rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
-               kgate: Optional[torch.Tensor] = None) -> None:
-    """Append [B, Lq, Hkv, 128] K/V into the cache at past_blocks; write mean-K (and gate-K)."""
+def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Optional[KV], v_cache: Optional[KV],
+               past_blocks: Sequence[int], kv_cap: int, kmean: Optional[torch.Tensor],
+               gate_wk: Optional[torch.Tensor] = None, rope_cos: Optional[torch.Tensor] = None,
+               rope_sin: Optional[torch.Tensor] = None, kgate: Optional[torch.Tensor] = None) -> None:
+    """Append [B, Lq, Hkv, 128] K/V into the cache at past_blocks; write mean-K (and gate-K).
+
+    With k_cache and v_cache None only the summaries are computed (nothing is copied)."""
     B, Lq, Hkv, _ = k_new.shape
     d = make_dims(B, Lq, Hkv, Hkv, kv_cap)
     kn = seq_layout(k_new, "k_new")
-    vn = seq_layout(v_new, "v_new")
+    if (k_cache is None) != (v_cache is None):
+        raise ValueError("k_cache and v_cache must both be given or both be None")
+    vn = seq_layout(v_new, "v_new") if k_cache is not None else None
     if kmean is not None:
         _need_cuda("kmean", kmean, torch.float32)
         if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
@@ -154,9 +158,11 @@ def cache_fill(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV, v_cache: K
             _need_cuda("rope_cos", rope_cos, torch.float32)
             _need_cuda("rope_sin", rope_sin, torch.float32)
             rope_rows = rope_cos.shape[0]
-    check(_hip.lib().ca_cache_fill(ctypes.byref(d), ctypes.byref(kn), ctypes.byref(vn), ctypes.byref(k_cache.layout),
-                                   ctypes.byref(v_cache.layout), past_array(past_blocks), _ptr(kmean), _ptr(gate_wk),
-                                   _ptr(rope_cos), _ptr(rope_sin), rope_rows, _ptr(kgate), _stream()))
+    check(_hip.lib().ca_cache_fill(ctypes.byref(d), ctypes.byref(kn), ctypes.byref(vn) if vn is not None else None,
+                                   ctypes.byref(k_cache.layout) if k_cache is not None else None,
+                                   ctypes.byref(v_cache.layout) if v_cache is not None else None,
+                                   past_array(past_blocks), _ptr(kmean), _ptr(gate_wk), _ptr(rope_cos),
+                                   _ptr(rope_sin), rope_rows, _ptr(kgate), _stream()))
 
 
 def pool_query(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, gate_wq: Optional[torch.Tensor] = None,

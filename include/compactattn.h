@@ -99,7 +99,8 @@ const char* ca_last_error(void);
  * mean of its 64 K rows into kmean[(b*Hkv + h)*kv_cap + kb][128] (sequential sum over the
  * 64 tokens, times 1/64).  If gate_wk is given ([Hkv, 128, 128], in x out) it also writes
  * kgate = RoPE(W_k[h]^T mean) (rope_cos/rope_sin: [rope_rows, 128] indexed by absolute
- * block id, may be NULL for no RoPE) into kgate with the kmean layout.
+ * block id, may be NULL for no RoPE) into kgate with the kmean layout.  With k_cache and
+ * v_cache both NULL nothing is copied and only the summaries are written (v_new unused).
  * Replaces: transformers DynamicCache.update concatenation
  * (compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:518-536),
  * compute_mean_vector / flash_prefill_compute_mean_k

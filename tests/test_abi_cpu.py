@@ -1,0 +1,174 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point the header declares,
+and its host-side validation rejects bad arguments before any launch (no GPU needed).
+Also the Python entry points' argument errors."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+from compactattention_amd import _hip, ops
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "compactattn.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ca_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_matches_exports():
+    names = declared_functions()
+    assert set(names) == set(_hip.EXPORTED), names
+    out = subprocess.run(["nm", "-D", "--defined-only", _hip.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = set(re.findall(r"\bT (ca_[a-z_0-9]+)\b", out))
+    assert set(names) <= exported, set(names) - exported
+
+
+def test_library_loads_and_reports_version():
+    lib = _hip.lib()
+    assert lib.ca_abi_version() == _hip.ABI_VERSION == 1
+
+
+def _dims(**kw):
+    d = dict(batch=1, q_len=128, num_q_heads=8, num_kv_heads=2, kv_cap=10)
+    d.update(kw)
+    return _hip.Dims(d["batch"], d["q_len"], d["num_q_heads"], d["num_kv_heads"], d["kv_cap"])
+
+
+FAKE = 1 << 20  # a 16-byte aligned address never dereferenced (validation fails first)
+
+
+def _seq(data=FAKE, sb=0, st=1024, sh=128):
+    return _hip.SeqLayout(data, sb, st, sh)
+
+
+def _kv(data=FAKE, sb=0, sh=0, sblk=8192, stok=128):
+    return _hip.KvLayout(data, sb, sh, sblk, stok, None, 0)
+
+
+def _past(*p):
+    return (ctypes.c_int32 * len(p))(*p)
+
+
+@pytest.mark.parametrize("dims,past,code,msg", [
+    (_dims(batch=0), (0,), _hip.CA_ERR_INVALID, "batch"),
+    (_dims(batch=65), (0,), _hip.CA_ERR_LIMIT, "batch"),
+    (_dims(q_len=100), (0,), _hip.CA_ERR_INVALID, "multiple of 64"),
+    (_dims(num_q_heads=7), (0,), _hip.CA_ERR_INVALID, "multiple"),
+    (_dims(num_q_heads=34, num_kv_heads=2), (0,), _hip.CA_ERR_LIMIT, "group size"),
+    (_dims(kv_cap=9), (8,), _hip.CA_ERR_INVALID, "exceeds kv_cap"),
+    (_dims(), (-1,), _hip.CA_ERR_INVALID, "< 0"),
+])
+def test_dims_validation(dims, past, code, msg):
+    lib = _hip.lib()
+    rc = lib.ca_attn_fwd(ctypes.byref(dims), ctypes.byref(_seq()), ctypes.byref(_kv()), ctypes.byref(_kv()), FAKE,
+                         16, FAKE, _past(*past), 0.1, ctypes.byref(_seq()), None, 1, None, 0, None)
+    assert rc == code
+    assert msg in _hip.last_error()
+
+
+def test_layout_and_workspace_validation():
+    lib = _hip.lib()
+    d = _dims()
+    args = lambda q, k, split, ws, wsb, scale=0.1, tstride=16: lib.ca_attn_fwd(  # noqa: E731
+        ctypes.byref(d), ctypes.byref(q), ctypes.byref(k), ctypes.byref(_kv()), FAKE, tstride, FAKE, _past(0),
+        scale, ctypes.byref(_seq()), None, split, ws, wsb, None)
+    assert args(_seq(data=FAKE + 2), _kv(), 1, None, 0) == _hip.CA_ERR_INVALID
+    assert "aligned" in _hip.last_error()
+    assert args(_seq(st=1023), _kv(), 1, None, 0) == _hip.CA_ERR_INVALID
+    assert args(_seq(), _kv(stok=0), 1, None, 0) == _hip.CA_ERR_INVALID
+    assert args(_seq(), _kv(), 1, None, 0, tstride=4) == _hip.CA_ERR_INVALID
+    assert args(_seq(), _kv(), 1, None, 0, scale=0.0) == _hip.CA_ERR_INVALID
+    assert args(_seq(), _kv(), 17, None, 0) == _hip.CA_ERR_INVALID
+    assert args(_seq(), _kv(), 2, None, 0) == _hip.CA_ERR_WORKSPACE
+    need = lib.ca_attn_workspace_size(ctypes.byref(d), _past(0), 2)
+    assert need == 2 * 1 * 2 * 128 * 4 * 129 * 4  # splits * B*Hkv * Lq*G rows * 129 floats
+    assert args(_seq(), _kv(), 2, FAKE, need - 1) == _hip.CA_ERR_WORKSPACE
+    assert lib.ca_attn_pick_splits(ctypes.byref(d), _past(0)) >= 1
+
+
+def test_rule_and_select_validation():
+    lib = _hip.lib()
+    d = _dims()
+    bad = _hip.SelectRule(8, 0, 0.0, 0.0, 0, 0, 0, 0)
+    rc = lib.ca_select_scores(ctypes.byref(d), FAKE, 0, 0, 0, 0, ctypes.byref(bad), _past(2), FAKE, None)
+    assert rc == _hip.CA_ERR_INVALID and "flags" in _hip.last_error()
+    neg = _hip.SelectRule(_hip.RULE_TOPK, -1, 0.0, 0.0, 0, 0, 0, 0)
+    rc = lib.ca_select_scores(ctypes.byref(d), FAKE, 0, 0, 0, 0, ctypes.byref(neg), _past(2), FAKE, None)
+    assert rc == _hip.CA_ERR_INVALID
+    ok = _hip.SelectRule(0, 0, 0.0, 0.0, 0, 0, 0, 0)
+    rc = lib.ca_select_scores(ctypes.byref(d), FAKE, 2, 0, 0, 0, ctypes.byref(ok), _past(2), FAKE, None)
+    assert rc == _hip.CA_ERR_INVALID and "dtype" in _hip.last_error()
+    rc = lib.ca_score_select(ctypes.byref(d), FAKE, FAKE, 0.1, ctypes.byref(ok), _past(2), FAKE, None, None)
+    assert rc == _hip.CA_ERR_INVALID and "scores" in _hip.last_error()
+    rc = lib.ca_union_compact(ctypes.byref(d), FAKE, 0, _past(2), None, None, FAKE, 4, FAKE, None)
+    assert rc == _hip.CA_ERR_INVALID and "table_stride" in _hip.last_error()
+
+
+def test_cache_fill_validation():
+    lib = _hip.lib()
+    d = _dims()
+    rc = lib.ca_cache_fill(ctypes.byref(d), ctypes.byref(_seq()), None, None, None, _past(0), None, None, None, None,
+                           0, None, None)
+    assert rc == _hip.CA_ERR_INVALID and "nothing to do" in _hip.last_error()
+    rc = lib.ca_cache_fill(ctypes.byref(d), ctypes.byref(_seq()), ctypes.byref(_seq()), ctypes.byref(_kv()),
+                           ctypes.byref(_kv()), _past(0), FAKE, FAKE, None, None, 0, None, None)
+    assert rc == _hip.CA_ERR_INVALID and "kgate" in _hip.last_error()
+    pt = _hip.KvLayout(FAKE, 0, 0, 8192, 128, FAKE, 1)
+    rc = lib.ca_cache_fill(ctypes.byref(d), ctypes.byref(_seq()), ctypes.byref(_seq()), ctypes.byref(pt),
+                           ctypes.byref(_kv()), _past(0), FAKE, None, None, None, 0, None, None)
+    assert rc == _hip.CA_ERR_INVALID and "page_table_stride" in _hip.last_error()
+
+
+def test_python_entry_points_reject_bad_arguments():
+    from compactattention_amd.modules.attention_forward_chunked_dense import (
+        chunked_prefill_column_dense_attention_forward, chunked_prefill_column_dense_attention_from_keep_block)
+    from compactattention_amd.modules.flashprefill_prefill import flashprefill_compactattn_prefill_full_kv
+
+    q = torch.zeros((1, 128, 8, 128), dtype=torch.bfloat16)
+    k = torch.zeros((1, 640, 2, 128), dtype=torch.bfloat16)
+    gate = torch.zeros((1, 8, 2, 10))
+    f = chunked_prefill_column_dense_attention_forward
+    with pytest.raises(ValueError, match="attn_gate_score is required"):
+        f(q, k, k, None, 128)
+    with pytest.raises(ValueError, match="query_length > 1"):
+        f(q, k, k, None, 1, attn_gate_score=gate)
+    with pytest.raises(ValueError, match="block_size must be positive"):
+        f(q, k, k, None, 128, attn_gate_score=gate, block_size=0)
+    with pytest.raises(ValueError, match="Unsupported indexed_impl"):
+        f(q, k, k, None, 128, attn_gate_score=gate, indexed_impl="nope")
+    with pytest.raises(ValueError, match="64-token blocks"):
+        f(q, k, k, None, 128, attn_gate_score=gate, block_size=128, num_key_value_groups=4)
+    with pytest.raises(ValueError, match="multiples of 64"):
+        f(q, k[:, :600], k[:, :600], None, 128, attn_gate_score=gate, num_key_value_groups=4)
+    with pytest.raises(ValueError, match="per-request threshold"):
+        f(q, k, k, None, 128, attn_gate_score=gate, threshold=torch.zeros(2), num_key_value_groups=4)
+    with pytest.raises(ValueError, match="Either keep_block"):
+        chunked_prefill_column_dense_attention_from_keep_block(q, k, k, None, None, 128, 0.1,
+                                                               num_key_value_groups=4)
+    with pytest.raises(ValueError, match="keep_block shape mismatch"):
+        chunked_prefill_column_dense_attention_from_keep_block(q, k, k, torch.zeros((1, 8, 9), dtype=torch.bool),
+                                                               None, 128, 0.1, num_key_value_groups=4)
+    with pytest.raises(ValueError, match="Unsupported indexed_impl"):
+        flashprefill_compactattn_prefill_full_kv(
+            q, k, k, None, softmax_scale=0.1, num_key_value_groups=4, block_size=64, attention_sink=2,
+            window_size=4, alpha=0.06, last_n_block=0, min_budget=0, pack_impl="torch", indexed_impl="x",
+            cache_fill_backend="auto")
+    with pytest.raises(ValueError, match="padded positions"):
+        mask = torch.ones((1, 640), dtype=torch.bool)
+        mask[0, 3] = False
+        f(q, k, k, mask, 128, attn_gate_score=gate, num_key_value_groups=4)
+
+
+def test_ops_reject_cpu_tensors():
+    q = torch.zeros((1, 128, 8, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        ops.pool_query(q, [0], 2)
