@@ -184,14 +184,26 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
     const float* kbase = khat + ((int64_t)row * s.cap + kb0) * kD;
     const int mrows = min(64, M - m0);
     const int krows = min(64, nkb - kb0);
-    for (int f = t; f < 64 * (kD / 4); f += 256) {
-        const int r = f >> 5, c4 = f & 31;
-        float4 qv = make_float4(0.f, 0.f, 0.f, 0.f);
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (r < mrows) qv = *reinterpret_cast<const float4*>(qbase + (int64_t)r * kD + c4 * 4);
-        if (r < krows) kv = *reinterpret_cast<const float4*>(kbase + (int64_t)r * kD + c4 * 4);
-        *reinterpret_cast<float4*>(qt + r * kPadRow + c4 * 4) = qv;
-        *reinterpret_cast<float4*>(kt + r * kPadRow + c4 * 4) = kv;
+    {
+        // all 16 loads of a thread in flight before the LDS stores
+        constexpr int kIters = 64 * (kD / 4) / 256;
+        float4 qv[kIters], kv[kIters];
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const int f = t + 256 * i;
+            const int r = f >> 5, c4 = f & 31;
+            qv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            kv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (r < mrows) qv[i] = *reinterpret_cast<const float4*>(qbase + (int64_t)r * kD + c4 * 4);
+            if (r < krows) kv[i] = *reinterpret_cast<const float4*>(kbase + (int64_t)r * kD + c4 * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < kIters; ++i) {
+            const int f = t + 256 * i;
+            const int r = f >> 5, c4 = f & 31;
+            *reinterpret_cast<float4*>(qt + r * kPadRow + c4 * 4) = qv[i];
+            *reinterpret_cast<float4*>(kt + r * kPadRow + c4 * 4) = kv[i];
+        }
     }
     __syncthreads();
     const int lane = t & 63;
@@ -235,9 +247,8 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
 }
 
 // ---------------------------------------------------------------------------------------
-// Row softmax + selection: one wavefront (workgroup of 64) per (b, h, qb) row, no block
-// barriers beyond the single wave's.  Softmax sum order: lane l sums kb = l, l+64, ...
-// ascending, then the tree part[l] += part[l+s], s = 32..1.
+// Row softmax + selection, one workgroup per (b, h, qb) row.  Softmax sum order: lane l
+// sums kb = l, l+64, ... ascending, then the tree part[l] += part[l+s], s = 32..1.
 struct SelectParams {
     Shape s;
     float* scores;          // [B*Hq*Qb][cap]: logits in, probabilities out (compute mode)
@@ -282,41 +293,117 @@ __device__ __forceinline__ int wave_excl_scan(int v, int lane) {
     return incl - v;
 }
 
+// The per-row selection runs one 256-thread workgroup per (b, h, qb) row; the row lives in
+// LDS.  Top-k is exact on the order (score desc, block id asc):
+//  1. a lower bound T_lo of the k-th largest key: the k-th largest of the 64 lane maxima
+//     (at least k distinct keys are >= it), for k <= 64;
+//  2. the keys >= T_lo (usually a few more than k) are gathered into a candidate list;
+//  3. the k-th largest key T and the id cut among keys equal to T are found over the list
+//     by bitwise construction with wave ballots.
+// A list that overflows (heavy ties, k > 64) falls back to the same search over the row.
+constexpr int kSelThreads = 256;
+constexpr int kSelWaves = kSelThreads / 64;
+constexpr int kCandSlots = 4;
+constexpr int kCandCap = 64 * kCandSlots;
+
+// Largest T with #{x >= T} >= k over the wave's S*64 values: the k-th largest (k >= 1).
+template <int S>
+__device__ __forceinline__ uint32_t wave_kth_largest(const uint32_t (&x)[S], int k) {
+    uint32_t T = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t c = T | (1u << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < S; ++i) cnt += __popcll(__ballot(x[i] >= c));
+        if (cnt >= k) T = c;
+    }
+    return T;
+}
+
+// Largest T with #{sel && id < T} < k over ids < 2^16: the k-th smallest selected id.
+template <int S>
+__device__ __forceinline__ int wave_kth_smallest_id(const int (&id)[S], const bool (&sel)[S], int k) {
+    int T = 0;
+    for (int bit = 15; bit >= 0; --bit) {
+        const int c = T | (1 << bit);
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < S; ++i) cnt += __popcll(__ballot(sel[i] && id[i] < c));
+        if (cnt < k) T = c;
+    }
+    return T;
+}
+
 template <bool kCompute>
-__global__ __launch_bounds__(64) void row_select_kernel(SelectParams p) {
+__global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p) {
     extern __shared__ float row[];  // [cap]
-    __shared__ int hist[256];
+    __shared__ float red_f[kSelWaves];
+    __shared__ int red_i[kSelWaves];
+    __shared__ uint32_t tmax[kSelThreads];
+    __shared__ uint32_t cand_key[kCandCap];
+    __shared__ int cand_id[kCandCap];
+    __shared__ int cand_n;
+    __shared__ uint32_t sel_lo, sel_T;
+    __shared__ int sel_cut;
     const Shape& s = p.s;
     const int rid = blockIdx.x;  // (b*Hq + h)*Qb + qb
     const int qb = rid % s.Qb;
     const int bh = rid / s.Qb;
     const int b = bh / s.Hq;
     const int h = bh - b * s.Hq;
-    const int lane = threadIdx.x;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
     const int P = p.pb.p[b];
     const int qabs = P + qb;
     const int n = qabs + 1;
     const int cap = s.cap;
+    constexpr float kNegInf = -__builtin_inff();
 
     if (kCompute) {
         float* srow = p.scores + (int64_t)rid * cap;
-        float m = -__builtin_inff();
-        for (int kb = lane; kb < n; kb += 64) {
-            const float v = srow[kb];
-            row[kb] = v;
-            m = fmaxf(m, v);
+        float m = kNegInf;
+        for (int base = 0; base < n; base += 4 * kSelThreads) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kb = base + t + kSelThreads * i;
+                v[i] = kb < n ? srow[kb] : kNegInf;
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kb = base + t + kSelThreads * i;
+                if (kb < n) row[kb] = v[i];
+                m = fmaxf(m, v[i]);
+            }
         }
         m = wave_max(m);
-        float part = 0.0f;
-        for (int kb = lane; kb < n; kb += 64) {
-            const float e = exp_fixed(row[kb] - m);
-            row[kb] = e;
-            part = part + e;
-        }
+        if (lane == 0) red_f[wave] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+        for (int kb = t; kb < n; kb += kSelThreads) row[kb] = exp_fixed(row[kb] - m);
+        __syncthreads();
+        if (wave == 0) {
+            // lane l sums kb = l, l + 64, ... in ascending order, then the fixed tree
+            float part = 0.0f;
+            for (int base = 0; base < n; base += 8 * 64) {
+                float e[8];
 #pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) part = part + __shfl_down(part, o, 64);
-        const float sum = __shfl(part, 0, 64);
-        for (int kb = lane; kb < cap; kb += 64) {
+                for (int i = 0; i < 8; ++i) {
+                    const int kb = base + lane + 64 * i;
+                    e[i] = kb < n ? row[kb] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (base + lane + 64 * i < n) part = part + e[i];
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) part = part + __shfl_down(part, o, 64);
+            if (lane == 0) red_f[0] = part;
+        }
+        __syncthreads();
+        const float sum = red_f[0];
+        for (int kb = t; kb < cap; kb += kSelThreads) {
             float v = 0.0f;
             if (kb < n) {
                 v = row[kb] / sum;
@@ -326,85 +413,158 @@ __global__ __launch_bounds__(64) void row_select_kernel(SelectParams p) {
         }
     } else {
         const int64_t off = b * p.ssb + h * p.ssh + qb * p.ssq;
-        for (int kb = lane; kb < n; kb += 64) {
-            float v;
-            if (p.dtype == 0)
-                v = static_cast<const float*>(p.scores_in)[off + kb];
-            else
-                v = bf16_to_f32(static_cast<const uint16_t*>(p.scores_in)[off + kb]);
-            row[kb] = v;
+        for (int base = 0; base < n; base += 4 * kSelThreads) {
+            float v[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kb = base + t + kSelThreads * i;
+                v[i] = 0.0f;
+                if (kb < n) {
+                    if (p.dtype == 0)
+                        v[i] = static_cast<const float*>(p.scores_in)[off + kb];
+                    else
+                        v[i] = bf16_to_f32(static_cast<const uint16_t*>(p.scores_in)[off + kb]);
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int kb = base + t + kSelThreads * i;
+                if (kb < n) row[kb] = v[i];
+            }
         }
     }
     __syncthreads();
 
+    // Row statistics: finite causal max (alpha rule), finite past count and the per-thread
+    // maximum past key (top-k bound).
     const ca_select_rule& rule = p.rule;
     const bool use_topk = (rule.flags & CA_RULE_TOPK) && rule.topk > 0 && P > 0;
-    float mx = 0.0f;
-    for (int kb = lane; kb < n; kb += 64) {
-        const float v = row[kb];
-        if (is_finite_f(v)) mx = fmaxf(mx, v);
-    }
-    const float rowmax = wave_max(mx);
-    const float alpha_cut = rule.alpha * rowmax;
-
-    bool take_all = false;
-    uint32_t T = 0;
-    int krem = 0;
-    if (use_topk) {
+    {
+        float mx = 0.0f;
         int nc = 0;
-        for (int kb = lane; kb < P; kb += 64) nc += is_finite_f(row[kb]) ? 1 : 0;
+        uint32_t kmax = 0;
+        for (int kb = t; kb < n; kb += kSelThreads) {
+            const float v = row[kb];
+            if (!is_finite_f(v)) continue;
+            mx = fmaxf(mx, v);
+            if (kb < P) {
+                ++nc;
+                kmax = max(kmax, order_key(v));
+            }
+        }
+        mx = wave_max(mx);
         nc = wave_sum_int(nc);
-        if (rule.topk >= nc) {
-            take_all = true;
-        } else {
-            uint32_t prefix = 0, pmask = 0;
-            krem = rule.topk;
-            for (int shift = 24; shift >= 0; shift -= 8) {
+        tmax[t] = kmax;
+        if (lane == 0) {
+            red_f[wave] = mx;
+            red_i[wave] = nc;
+        }
+        if (t == 0) cand_n = 0;
+    }
+    __syncthreads();
+    const float rowmax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    const int ncand = red_i[0] + red_i[1] + red_i[2] + red_i[3];
+    const float alpha_cut = rule.alpha * rowmax;
+    const bool take_all = use_topk && rule.topk >= ncand;
+    const bool cut = use_topk && !take_all;
+    const int k = rule.topk;
+
+    if (cut) {
+        if (wave == 0) {
+            uint32_t lo = 0;
+            if (k <= 64) {
+                const uint32_t m[1] = {max(max(tmax[lane], tmax[lane + 64]),
+                                           max(tmax[lane + 128], tmax[lane + 192]))};
+                lo = wave_kth_largest<1>(m, k);
+            }
+            if (lane == 0) sel_lo = lo;
+        }
+        __syncthreads();
+        const uint32_t lo = sel_lo;
+        for (int kb = t; kb < P; kb += kSelThreads) {
+            const float v = row[kb];
+            if (!is_finite_f(v)) continue;
+            const uint32_t key = order_key(v);
+            if (key < lo) continue;
+            const int slot = atomicAdd(&cand_n, 1);
+            if (slot < kCandCap) {
+                cand_key[slot] = key;
+                cand_id[slot] = kb;
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            const int nl = cand_n;
+            uint32_t T;
+            int eq_cut;
+            if (nl <= kCandCap) {
+                uint32_t x[kCandSlots];
+                int id[kCandSlots];
+                bool eq[kCandSlots];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) hist[lane + 64 * i] = 0;
-                __syncthreads();
+                for (int i = 0; i < kCandSlots; ++i) {
+                    const int j = lane + 64 * i;
+                    x[i] = j < nl ? cand_key[j] : 0u;
+                    id[i] = j < nl ? cand_id[j] : 0;
+                }
+                T = wave_kth_largest<kCandSlots>(x, k);
+                int gt = 0;
+#pragma unroll
+                for (int i = 0; i < kCandSlots; ++i) {
+                    gt += __popcll(__ballot(x[i] > T));
+                    eq[i] = x[i] == T;
+                }
+                eq_cut = wave_kth_smallest_id<kCandSlots>(id, eq, k - gt);
+            } else {
+                T = 0;
+                for (int bit = 31; bit >= 0; --bit) {
+                    const uint32_t c = T | (1u << bit);
+                    int cnt = 0;
+                    for (int kb = lane; kb < P; kb += 64) {
+                        const float v = row[kb];
+                        cnt += (is_finite_f(v) && order_key(v) >= c) ? 1 : 0;
+                    }
+                    if (wave_sum_int(cnt) >= k) T = c;
+                }
+                int gt = 0;
                 for (int kb = lane; kb < P; kb += 64) {
                     const float v = row[kb];
-                    if (!is_finite_f(v)) continue;
-                    const uint32_t key = order_key(v);
-                    if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
+                    gt += (is_finite_f(v) && order_key(v) > T) ? 1 : 0;
                 }
-                __syncthreads();
-                // lane l owns digits 255-4l, 254-4l, 253-4l, 252-4l (descending)
-                int c[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) c[i] = hist[255 - 4 * lane - i];
-                const int excl = wave_excl_scan(c[0] + c[1] + c[2] + c[3], lane);
-                int run = excl, found = -1, above = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    if (found < 0 && c[i] > 0 && run < krem && krem <= run + c[i]) {
-                        found = 255 - 4 * lane - i;
-                        above = run;
+                const int krem = k - wave_sum_int(gt);
+                // the krem-th key equal to T in ascending block order
+                const uint64_t lt_mask = (1ull << lane) - 1ull;
+                int seen = 0;
+                eq_cut = P;
+                for (int base = 0; base < P; base += 64) {
+                    const int kb = base + lane;
+                    const float v = kb < P ? row[kb] : 0.0f;
+                    const bool e = kb < P && is_finite_f(v) && order_key(v) == T;
+                    const uint64_t bal = __ballot(e);
+                    const int cnt = __popcll(bal);
+                    if (seen + cnt >= krem) {
+                        const uint64_t who = __ballot(e && seen + __popcll(bal & lt_mask) == krem - 1);
+                        eq_cut = base + __ffsll(static_cast<unsigned long long>(who)) - 1;
+                        break;
                     }
-                    run += c[i];
+                    seen += cnt;
                 }
-                const uint64_t who = __ballot(found >= 0);
-                const int src = __ffsll(static_cast<unsigned long long>(who)) - 1;
-                const int digit = __shfl(found, src, 64);
-                const int abv = __shfl(above, src, 64);
-                prefix |= static_cast<uint32_t>(digit) << shift;
-                pmask |= 255u << shift;
-                krem -= abv;
-                __syncthreads();
             }
-            T = prefix;
+            if (lane == 0) {
+                sel_T = T;
+                sel_cut = eq_cut;
+            }
         }
+        __syncthreads();
     }
+    const uint32_t T = cut ? sel_T : 0u;
+    const int eq_cut = cut ? sel_cut : -1;
 
     uint32_t* out = p.rowmask + (int64_t)rid * s.words;
     const int chunks = (s.words + 1) / 2;
-    const uint64_t lt_mask = (1ull << lane) - 1ull;
-    int eq_base = 0;
-    for (int c = 0; c < chunks; ++c) {
+    for (int c = wave; c < chunks; c += kSelWaves) {
         const int kb = c * 64 + lane;
         bool keep = false;
-        bool eq = false;
         if (kb < n) {
             const float v = row[kb];
             const bool fin = is_finite_f(v);
@@ -418,14 +578,10 @@ __global__ __launch_bounds__(64) void row_select_kernel(SelectParams p) {
                     keep = true;
                 } else {
                     const uint32_t key = order_key(v);
-                    if (key > T) keep = true;
-                    eq = key == T;
+                    if (key > T || (key == T && kb <= eq_cut)) keep = true;
                 }
             }
         }
-        const uint64_t eqb = __ballot(eq);
-        if (eq && eq_base + __popcll(eqb & lt_mask) < krem) keep = true;
-        eq_base += __popcll(eqb);
         const uint64_t bal = __ballot(keep);
         if (lane == 0) out[2 * c] = static_cast<uint32_t>(bal);
         if (lane == 1 && 2 * c + 1 < s.words) out[2 * c + 1] = static_cast<uint32_t>(bal >> 32);
@@ -588,9 +744,9 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
     const size_t lds = score_select_lds_bytes(s, compute);
     dim3 grid(s.B * s.Hq * s.Qb);
     if (compute)
-        hipLaunchKernelGGL(row_select_kernel<true>, grid, dim3(64), lds, stream, p);
+        hipLaunchKernelGGL(row_select_kernel<true>, grid, dim3(kSelThreads), lds, stream, p);
     else
-        hipLaunchKernelGGL(row_select_kernel<false>, grid, dim3(64), lds, stream, p);
+        hipLaunchKernelGGL(row_select_kernel<false>, grid, dim3(kSelThreads), lds, stream, p);
     return hipGetLastError();
 }
 

@@ -166,6 +166,42 @@ def test_select_scores_ties_and_nonfinite(gpu, dtype):
         assert np.array_equal(unpack_rowmask(rowmask, cap), ref), rule
 
 
+@pytest.mark.parametrize("case", ["two_values", "k_gt_64", "k_eq_64", "sparse_finite", "negative"])
+def test_select_topk_search_paths(gpu, case):
+    """Top-k through each branch of the kernel's search: the candidate list after the
+    lane-maximum bound (k <= 64), its overflow into the full-row search (heavy ties) and
+    k > 64; also rows where few lanes hold finite candidates and all-negative scores."""
+    _print_case(test="select_topk_paths", case=case)
+    B, Hkv, G, Lq = 1, 2, 2, 128
+    Hq = Hkv * G
+    past = [700]
+    qb = Lq // 64
+    cap = past[0] + qb
+    g = torch.Generator().manual_seed(17)
+    k = 10
+    if case == "two_values":  # ~350 keys equal to the maximum: the list overflows
+        s = (torch.rand((B, Hq, qb, cap), generator=g) < 0.5).float()
+    elif case == "k_gt_64":
+        s = torch.rand((B, Hq, qb, cap), generator=g)
+        k = 100
+    elif case == "k_eq_64":
+        s = torch.randint(0, 50, (B, Hq, qb, cap), generator=g).float()
+        k = 64
+    elif case == "sparse_finite":  # finite candidates only in lanes 0..9 of each 64
+        s = torch.rand((B, Hq, qb, cap), generator=g)
+        s[..., (torch.arange(cap) % 64) >= 10] = float("nan")
+        k = 30
+    else:
+        s = -torch.rand((B, Hq, qb, cap), generator=g) * 5
+        s[..., 5] = -0.0
+        s[..., 6] = 0.0
+    rule = oracle.Rule(topk=k)
+    rowmask = ops.select_scores(s.to(gpu), _ops_rule(rule), past, Hkv, cap, Lq)
+    ref = oracle.select_rows(s.numpy(), past, rule)
+    assert ref[..., :past[0]].sum(axis=-1).max() == k
+    assert np.array_equal(unpack_rowmask(rowmask, cap), ref)
+
+
 # ----------------------------------------------------------------------------- union + tables
 @pytest.mark.parametrize("last_n_block", [0, 2])
 @pytest.mark.parametrize("G", [1, 4, 7])
