@@ -30,6 +30,10 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
 
+def progress(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def parse():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -42,7 +46,13 @@ def parse():
     ap.add_argument("--kv-heads", type=int, default=8)
     ap.add_argument("--sweep", default="0.10,0.25,0.50", help="keep ratios for the attention sweep ('' = off)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=4, help="query tokens in the CPU attention sample")
+    ap.add_argument("--cpu-tokens", type=int, default=320, help="query tokens in the CPU attention sample")
+    ap.add_argument("--no-model", action="store_true", help="skip the config-3 whole-model prefill")
+    ap.add_argument("--model-tokens", type=int, default=131072)
+    ap.add_argument("--model-chunk", type=int, default=2048)
+    ap.add_argument("--model-layers", type=int, default=32)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three plain 256 MiB device copies (the HBM counter calibration under rocprofv3)")
     return ap.parse_args()
 
 
@@ -53,6 +63,15 @@ def main() -> int:
                           "n_gpus": args.gpus}))
         return 2
     import torch
+
+    if args.copy_calibration:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda:0")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": a.numel(), "copies": 3}))
+        return 0
 
     from compactattention_amd import ops
     from compactattention_amd.synthetic import make_chunk_device
@@ -111,6 +130,7 @@ def main() -> int:
                 hi = mid - 1
         return best
 
+    progress("cache filled; calibrating the top-k")
     topk, _ = calibrate(args.keep)
     rule = ops.Rule(topk=topk, sink_blocks=1, local_blocks=2)
 
@@ -132,6 +152,7 @@ def main() -> int:
     elapsed = time.perf_counter() - t0
     us_per_chunk = elapsed / args.steps * 1e6
 
+    progress(f"timed {args.steps} steps: {us_per_chunk:.1f} us per chunk")
     table, counts = step()
     torch.cuda.synchronize()
     cnt = counts.cpu()
@@ -237,17 +258,91 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(attn_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
             "kernel": "attn_fwd_kernel (+ split merge)",
             "flops_per_launch": flops,
         },
     }
 
     if not args.no_cpu_baseline:
+        progress("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(ch, kmean, topk, scale, args.cpu_tokens)
+    if not args.no_model:
+        del ch, kc, vc, K, V, kmean, ws, dws
+        torch.cuda.empty_cache()
+        result["model_prefill"] = model_prefill(args.model_tokens, args.model_chunk, args.model_layers, dev)
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+def measured_traffic():
+    """HBM bytes per attention launch (attn_fwd + merge) from the committed rocprofv3 PMC
+    record, used only while the kernel source is the one that was measured."""
+    import hashlib
+
+    rec_path = os.path.join(ROOT, "profiles", "attn_fwd_cfg2_traffic.json")
+    src = os.path.join(ROOT, "compactattention_amd", "csrc", "ca_attn.hip")
+    try:
+        rec = json.load(open(rec_path))
+        sha = hashlib.sha256(open(src, "rb").read()).hexdigest()
+    except OSError:
+        return None
+    if rec.get("kernel_source_sha256") != sha:
+        return None
+    return rec["bytes_per_launch"]
+
+
+def model_prefill(tokens, chunk, layers, dev):
+    """whole-model chunked prefill of a Llama-3.1-8B-shaped decoder with
+    random N(0, 0.02) bf16 weights, AttnGate (Seer selector, softmax threshold 5e-3 + sink
+    block + 2 local blocks) at every layer, first chunk dense; next to the same model with
+    every chunk dense (identity tables)."""
+    import torch
+
+    from compactattention_amd.chunked_prefill import run_chunked_prefill_once, synthetic_prompt
+    from compactattention_amd.prefill_sparse.llama import SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaConfig
+
+    cfg = SeerAttnLlamaConfig(num_hidden_layers=layers, max_position_embeddings=max(tokens, 131072))
+    model = SeerAttnLlamaChunkedDenseForCausalLM(cfg, device=dev)
+    model.init_weights(seed=1234)
+    ids = synthetic_prompt(1, tokens, cfg.vocab_size, 1234 + 131072 * 104729, dev)
+    cache = model.new_cache(1, tokens)
+    progress("model prefill: warm-up")
+    run_chunked_prefill_once(model, ids[:, :min(tokens, 4 * chunk)], chunk, cache)  # warm-up
+    _, compact_s = run_chunked_prefill_once(model, ids, chunk, cache)
+    progress(f"model prefill: compactattn {compact_s:.2f} s")
+    # keep ratio of the last chunk, every layer
+    for layer in model.model.layers:
+        layer.self_attn.compactattn_debug = True
+    run_chunked_prefill_once(model, ids, chunk, cache)
+    qb = chunk // 64
+    keeps = []
+    for st in model.attention_stats():
+        if st and st["past_blocks"] > 0:
+            keeps.append(float((st["counts"].float() - qb).mean().item()) / st["past_blocks"])
+    for layer in model.model.layers:
+        layer.self_attn.compactattn_debug = False
+    cfg.seerattn_chunked_prefill_force_dense = True
+    _, dense_s = run_chunked_prefill_once(model, ids, chunk, cache)
+    progress(f"model prefill: dense {dense_s:.2f} s")
+    linear_flops = 2.0 * tokens * sum(p.numel() for n, p in model.named_parameters()
+                                      if n.startswith("model.layers.") and "proj" in n and "attn_gate" not in n)
+    del model, cache
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"config 3: Llama-3.1-8B-shaped decoder ({layers} layers, hidden 4096, 32 Q / 8 KV heads, "
+                    f"SwiGLU 14336, vocab 128256), random N(0,0.02) bf16 weights, {tokens}-token synthetic prompt, "
+                    f"chunk {chunk}, AttnGate Qavg_Kavg + threshold 5e-3 + sink + 2 local blocks at every layer, "
+                    "first chunk dense, logits of the last token only",
+        "tok_per_s": round(tokens / compact_s, 1),
+        "seconds": round(compact_s, 3),
+        "dense_tok_per_s": round(tokens / dense_s, 1),
+        "dense_seconds": round(dense_s, 3),
+        "speedup_vs_dense": round(dense_s / compact_s, 3),
+        "keep_ratio_last_chunk": round(sum(keeps) / max(len(keeps), 1), 4),
+        "linear_tflops_per_s": round(linear_flops / compact_s / 1e12, 1),
+    }
 
 
 def cpu_baseline(ch, kmean, topk, scale, n_tok):
@@ -285,13 +380,14 @@ def cpu_baseline(ch, kmean, topk, scale, n_tok):
     t2 = time.perf_counter()
     select_s = t1 - t0
     attn_s = (t2 - t1) * (Lq / n_tok)
+    scale_note = f"x{Lq / n_tok:g}"
     return {
         "value": round((select_s + attn_s) * 1e6, 1),
         "unit": "us per chunk",
         "cores": oracle.num_threads(),
         "kind": "port",
         "sample": f"oracle selection path for the whole chunk ({select_s:.2f} s) + attention for the last "
-                  f"{n_tok} of {Lq} query tokens x all heads ({t2 - t1:.2f} s), attention extrapolated x{Lq // n_tok}",
+                  f"{n_tok} of {Lq} query tokens x all heads ({t2 - t1:.2f} s), attention extrapolated {scale_note}",
     }
 
 

@@ -10,15 +10,17 @@
 // Work decomposition
 //  - The G query heads of a KV group share the group's block table, so a KV row
 //    (request, kv head) owns Lq*G "packed" query rows r = t*G + g (token t, head g).
-//  - A workgroup (4 waves) takes 256 packed rows; each wave keeps 64 rows (two 32-row MFMA
-//    tiles) for the whole KV loop: Q in VGPRs, O^T in accumulators.
+//  - A workgroup (4 waves) takes 128 packed rows; each wave keeps 32 rows (one 32x32 MFMA
+//    tile) for the whole KV loop: Q in VGPRs, O^T in accumulators.  Two workgroups share a
+//    CU, so each SIMD runs two waves whose softmax and MFMA phases overlap.
 //  - Scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q from VGPRs), so the
 //    softmax output lands in exactly the VGPR layout the second product's B operand needs:
 //    O^T += V^T P^T (A = V^T from LDS).  Inside each 32-key S^T tile the A-row -> key map
 //    swaps bits 2 and 3 of the row index, which makes every lane's 8 P values 8 consecutive
 //    keys, i.e. one 16-byte V^T read.
-//  - K blocks are stored in LDS row-major with a 16-byte-chunk XOR swizzle; V blocks are
-//    transposed on their way into LDS (register 8x4 transpose) so V^T rows are contiguous.
+//  - K blocks are stored in LDS row-major with a 272-byte row pitch (conflict-free fragment
+//    reads at immediate offsets); V blocks are transposed on their way into LDS (register
+//    8x4 transpose) into V^T rows with 16-byte chunks XOR-swizzled by row.
 //  - Two LDS stages: the next block's global loads are in flight while the current block is
 //    computed.  Optional split of each row's block list (split-KV) with an LSE merge.
 //  - Workgroup ids are remapped so consecutive work items (same KV row) share an XCD and
@@ -35,6 +37,7 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -282,6 +285,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         const float m_use = m_run == -__builtin_inff() ? 0.0f : m_run;
         bf16x8_t pf[4];
         float rs = 0.0f;
+        const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
             f32x8_t pv8;
@@ -289,8 +293,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
             for (int i = 0; i < 8; ++i)
                 pv8[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[s4 >> 1][8 * (s4 & 1) + i], sl2, -m_use));
             pf[s4] = __builtin_convertvector(pv8, bf16x8_t);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) rs += pv8[i];
+            // the normaliser sums the bf16-rounded weights the PV product uses
+            rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[s4], pf[s4], 0, 1), ones, rs, false);
+            rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[s4], pf[s4], 2, 3), ones, rs, false);
+            rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[s4], pf[s4], 4, 5), ones, rs, false);
+            rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[s4], pf[s4], 6, 7), ones, rs, false);
         }
         l_run += rs;  // this lane's half of the row; combined across lanes n, n+32 at the end
 #pragma unroll

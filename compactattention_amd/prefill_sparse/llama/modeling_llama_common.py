@@ -1,0 +1,200 @@
+"""Llama decoder pieces shared by the compactattn models, plus the per-layer paged cache.
+
+The reference builds its compactattn models on transformers' Llama classes
+(compact_attn/prefill_sparse/llama/modeling_llama_seerattn.py: SeerAttnLlamaDecoderLayer,
+SeerAttnLlamaModel, SeerAttnLlamaForCausalLM) with a DynamicCache.  Here the decoder is
+written directly on PyTorch-ROCm (projections are hipBLASLt GEMMs through nn.Linear), the
+attention modules run the HIP compactattn kernels, and the cache is a set of
+preallocated per-layer PagedKVCache objects, so a chunk's K/V is appended in place
+instead of re-concatenated.
+
+Shapes: hidden states [B, L, hidden]; Q/K/V [B, L, heads, 128].  Rotary tables are fp32,
+computed once for every position ([max_positions, 128]); the block tables the gate uses
+take the row of each block's first token (modeling_llama_seerattn.py:896-897).
+"""
+from __future__ import annotations
+
+from typing import List, Optional, Tuple, Type
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from ...kv_cache import PagedKVCache
+from .configuration_llama_seerattn import SeerAttnLlamaConfig
+
+BLOCK = 64
+
+
+class LlamaRMSNorm(nn.Module):
+    def __init__(self, hidden_size: int, eps: float, device=None, dtype=torch.bfloat16):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=dtype))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        # statistics in fp32, as transformers' LlamaRMSNorm
+        y = F.rms_norm(x.float(), (x.shape[-1],), eps=self.eps)
+        return self.weight * y.to(x.dtype)
+
+
+class LlamaMLP(nn.Module):
+    def __init__(self, config: SeerAttnLlamaConfig, device=None, dtype=torch.bfloat16):
+        super().__init__()
+        kw = dict(bias=False, device=device, dtype=dtype)
+        self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, **kw)
+        self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, **kw)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, **kw)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class LlamaRotaryEmbedding(nn.Module):
+    """cos/sin tables [max_positions, head_dim] (fp32) with the rotate_half layout."""
+
+    def __init__(self, config: SeerAttnLlamaConfig, device=None):
+        super().__init__()
+        d = config.head_dim
+        inv_freq = 1.0 / (config.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+        pos = torch.arange(config.max_position_embeddings, dtype=torch.float64)
+        freqs = torch.outer(pos, inv_freq)
+        emb = torch.cat([freqs, freqs], dim=-1)
+        self.register_buffer("cos", emb.cos().float().to(device), persistent=False)
+        self.register_buffer("sin", emb.sin().float().to(device), persistent=False)
+        self.register_buffer("block_cos", self.cos[::BLOCK].contiguous(), persistent=False)
+        self.register_buffer("block_sin", self.sin[::BLOCK].contiguous(), persistent=False)
+
+    def tokens(self, start: int, length: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        if start + length > self.cos.shape[0]:
+            raise ValueError(f"positions up to {start + length} exceed max_position_embeddings {self.cos.shape[0]}")
+        return self.cos[start:start + length], self.sin[start:start + length]
+
+    def blocks(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        return self.block_cos, self.block_sin
+
+
+def rotate_half(x: torch.Tensor) -> torch.Tensor:
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
+                         ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """q [B, L, Hq, D], k [B, L, Hkv, D], cos/sin [L, D] fp32 -> rotated (input dtype).
+    Same formula as the reference's apply_rotary_pos_emb (modules/common.py:29-81),
+    evaluated in fp32."""
+    c = cos[None, :, None, :]
+    s = sin[None, :, None, :]
+    qf, kf = q.float(), k.float()
+    return (qf * c + rotate_half(qf) * s).to(q.dtype), (kf * c + rotate_half(kf) * s).to(k.dtype)
+
+
+class ChunkedPrefillCache:
+    """One PagedKVCache per layer (all layers advance together)."""
+
+    def __init__(self, config: SeerAttnLlamaConfig, batch: int, max_tokens: int, device, with_kmean: bool,
+                 with_kgate: bool):
+        max_tokens = -(-max_tokens // BLOCK) * BLOCK
+        self.layers: List[PagedKVCache] = [
+            PagedKVCache(batch, config.num_key_value_heads, max_tokens, device, with_kmean=with_kmean,
+                         with_kgate=with_kgate)
+            for _ in range(config.num_hidden_layers)
+        ]
+
+    def layer(self, idx: int) -> PagedKVCache:
+        return self.layers[idx]
+
+    def get_seq_length(self) -> int:
+        return self.layers[0].length
+
+    def reset(self) -> None:
+        for c in self.layers:
+            c.reset()
+
+
+class CompactAttnLlamaDecoderLayer(nn.Module):
+    def __init__(self, config: SeerAttnLlamaConfig, layer_idx: int, attn_cls: Type[nn.Module], device=None):
+        super().__init__()
+        self.self_attn = attn_cls(config, layer_idx, device=device)
+        self.mlp = LlamaMLP(config, device=device)
+        self.input_layernorm = LlamaRMSNorm(config.hidden_size, config.rms_norm_eps, device=device)
+        self.post_attention_layernorm = LlamaRMSNorm(config.hidden_size, config.rms_norm_eps, device=device)
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings, block_position_embeddings,
+                past_key_value: ChunkedPrefillCache) -> torch.Tensor:
+        residual = hidden_states
+        h = self.input_layernorm(hidden_states)
+        h = self.self_attn(h, position_embeddings, None, past_key_value=past_key_value,
+                           block_position_embeddings=block_position_embeddings)[0]
+        hidden_states = residual + h
+        residual = hidden_states
+        h = self.mlp(self.post_attention_layernorm(hidden_states))
+        return residual + h
+
+
+class CompactAttnLlamaModel(nn.Module):
+    def __init__(self, config: SeerAttnLlamaConfig, attn_cls: Type[nn.Module], device=None):
+        super().__init__()
+        self.config = config
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size, device=device, dtype=torch.bfloat16)
+        self.layers = nn.ModuleList([CompactAttnLlamaDecoderLayer(config, i, attn_cls, device=device)
+                                     for i in range(config.num_hidden_layers)])
+        self.norm = LlamaRMSNorm(config.hidden_size, config.rms_norm_eps, device=device)
+        self.rotary_emb = LlamaRotaryEmbedding(config, device=device)
+
+    def forward(self, input_ids: torch.Tensor, past_key_values: ChunkedPrefillCache) -> torch.Tensor:
+        start = past_key_values.get_seq_length()
+        h = self.embed_tokens(input_ids)
+        pos = self.rotary_emb.tokens(start, input_ids.shape[1])
+        blk = self.rotary_emb.blocks()
+        for layer in self.layers:
+            h = layer(h, pos, blk, past_key_values)
+        return self.norm(h)
+
+
+class CompactAttnLlamaForCausalLM(nn.Module):
+    """Decoder + LM head; forward(input_ids, past_key_values, logits_to_keep) runs one
+    prefill chunk (the reference runtime's call, chunked_prefill_runtime.py:1168-1203)."""
+
+    attn_cls: Type[nn.Module] = nn.Module
+    cache_with_kmean = False
+    cache_with_kgate = False
+
+    def __init__(self, config: SeerAttnLlamaConfig, device=None):
+        super().__init__()
+        config.validate()
+        self.config = config
+        self.model = CompactAttnLlamaModel(config, self.attn_cls, device=device)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False, device=device, dtype=torch.bfloat16)
+
+    @torch.no_grad()
+    def init_weights(self, seed: int = 1234) -> None:
+        """Random N(0, initializer_range) weights (unit RMSNorm weights), drawn on the
+        parameters' device from one seeded generator."""
+        dev = self.lm_head.weight.device
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        std = self.config.initializer_range
+        for name, p in self.named_parameters():
+            if name.endswith("layernorm.weight") or name == "model.norm.weight":
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std, generator=g)
+
+    def new_cache(self, batch: int, max_tokens: int) -> ChunkedPrefillCache:
+        return ChunkedPrefillCache(self.config, batch, max_tokens, self.lm_head.weight.device,
+                                   with_kmean=self.cache_with_kmean, with_kgate=self.cache_with_kgate)
+
+    @torch.no_grad()
+    def forward(self, input_ids: torch.Tensor, past_key_values: ChunkedPrefillCache,
+                logits_to_keep: int = 1) -> torch.Tensor:
+        if input_ids.shape[1] < 2:
+            raise ValueError("decode steps (one token) are not supported by the compactattn prefill path")
+        h = self.model(input_ids, past_key_values)
+        if logits_to_keep > 0:
+            h = h[:, -logits_to_keep:]
+        return self.lm_head(h)
+
+    def attention_stats(self) -> List[Optional[dict]]:
+        return [layer.self_attn._compactattn_last_stats for layer in self.model.layers]

@@ -1,0 +1,105 @@
+"""FlashPrefill compactattn Llama attention and model on the HIP kernels.
+
+Mirrors LlamaFlashPrefillCompactAttnAttention.forward
+(compact_attn/prefill_sparse/llama/modeling_llama_flashprefill_compactattn.py:152-341):
+q/k/v projections, RoPE, cache update with the per-layer mean-K cache (:121-150), then
+flashprefill_compactattn_prefill_full_kv for chunks with past context and dense attention
+for the first chunk, then o_proj.
+
+Execution per chunk: one ca_cache_fill appends the RoPE'd K/V pages and writes the fp32
+mean-K of the new blocks; ca_pool_query pools the RoPE'd queries; ca_score_select scores
+pooled Q.K blocks (softmax over causal key blocks, scale 1/sqrt(128)) and applies the
+FlashPrefill row rule (alpha * row max, sink, window, optional top-k budget);
+ca_union_compact leaves the last last_n_block query blocks out of the union; ca_attn_fwd
+attends over the cache pages.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Tuple
+
+import torch
+from torch import nn
+
+from ... import ops
+from ...modules._core import COMPACTATTN_VERSION
+from ...modules.flashprefill_prefill import flashprefill_rule
+from .configuration_llama_seerattn import SeerAttnLlamaConfig
+from .modeling_llama_common import ChunkedPrefillCache, CompactAttnLlamaForCausalLM, apply_rotary_pos_emb
+
+BLOCK = 64
+
+
+class LlamaFlashPrefillCompactAttnAttention(nn.Module):
+    def __init__(self, config: SeerAttnLlamaConfig, layer_idx: int, device=None):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.head_dim = config.head_dim
+        self.num_heads = config.num_attention_heads
+        self.num_key_value_heads = config.num_key_value_heads
+        self.num_key_value_groups = config.num_key_value_groups
+        self.scaling = self.head_dim ** -0.5
+        kw = dict(bias=False, device=device, dtype=torch.bfloat16)
+        self.q_proj = nn.Linear(config.hidden_size, self.num_heads * self.head_dim, **kw)
+        self.k_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
+        self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
+        self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
+        self.compactattn_version = COMPACTATTN_VERSION
+        self.compactattn_debug = False
+        self._compactattn_last_stats = None
+
+    def _selection_rule(self) -> ops.Rule:
+        c = self.config
+        return flashprefill_rule(c.seerattn_flashprefill_attention_sink, c.seerattn_flashprefill_window_size,
+                                 c.seerattn_flashprefill_alpha, c.seerattn_flashprefill_last_n_block,
+                                 c.seerattn_flashprefill_min_budget)
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings: Tuple[torch.Tensor, torch.Tensor],
+                attention_mask: Optional[torch.Tensor] = None, past_key_value: Optional[ChunkedPrefillCache] = None,
+                cache_position: Optional[torch.LongTensor] = None, **kwargs):
+        del cache_position, kwargs
+        if past_key_value is None:
+            raise ValueError("the compactattn prefill path needs a ChunkedPrefillCache")
+        if attention_mask is not None and not bool(attention_mask.all()):
+            raise ValueError("padded positions are not supported by the compactattn prefill path")
+        B, L, _ = hidden_states.shape
+        if L % BLOCK:
+            raise ValueError("chunk lengths must be multiples of 64 tokens")
+        q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim)
+        k = self.k_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
+        v = self.v_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
+        cos, sin = position_embeddings
+        query_states, key_states = apply_rotary_pos_emb(q, k, cos, sin)
+
+        cache = past_key_value.layer(self.layer_idx)
+        past = cache.append(key_states, v.contiguous())  # pages + mean-K of the new blocks
+        P = [past] * B
+        dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
+        if dense:
+            table, counts = ops.dense_table(P, L, self.num_heads, self.num_key_value_heads, cache.cap,
+                                            query_states.device)
+        else:
+            rule = self._selection_rule()
+            qhat = ops.pool_query(query_states, P, cache.cap, num_kv_heads=self.num_key_value_heads)
+            rowmask, _ = ops.score_select(qhat, cache.kmean, 1.0 / math.sqrt(self.head_dim), rule, P,
+                                          self.num_key_value_heads, cache.cap)
+            table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap,
+                                                    last_n_block=rule.last_n_block)
+        K, V = cache.layouts()
+        out = ops.attn_fwd(query_states, K, V, table, counts, P, self.scaling, cache.cap, self.num_key_value_heads)
+        out = self.o_proj(out.reshape(B, L, -1))
+        if self.compactattn_debug:
+            self._compactattn_last_stats = {
+                "path": "dense_fallback" if dense else "flashprefill_chunked_selected",
+                "past_blocks": past, "table": table, "counts": counts,
+                "compactattn_version": self.compactattn_version,
+            }
+        else:
+            self._compactattn_last_stats = None
+        return out, 0.0, None, None, None
+
+
+class SeerAttnLlamaFlashPrefillCompactAttnForCausalLM(CompactAttnLlamaForCausalLM):
+    attn_cls = LlamaFlashPrefillCompactAttnAttention
+    cache_with_kmean = True

@@ -1,0 +1,142 @@
+"""Seer (AttnGate) compactattn Llama attention and model on the HIP kernels.
+
+Mirrors LlamaSeerAttentionChunkedDense.forward
+(compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:547-938):
+q/k/v projections, RoPE, cache update, the gate K-block cache (:385-478), then for a
+chunk with past context the compactattn forward (threshold on the AttnGate softmax scores,
+Q-block union, GQA union, indexed attention), for the first chunk dense causal attention,
+then o_proj.  The module returns the reference's 5-tuple (attn_output, mask_loss, None,
+attn_gate_output, ground_truth_mask); inference only.
+
+Execution per chunk (B requests advancing together, L tokens, P past blocks):
+  1. paged append of RoPE'd K and V (ca_cache_fill, copy only);
+  2. gate K summaries of the new blocks from the pre-RoPE K (ca_cache_fill summaries:
+     block mean -> per-KV-head 128x128 projection -> block RoPE) into the cache's kgate;
+  3. pooled, projected, rotated query blocks (ca_pool_query with the gate's W_q);
+  4. gate scores + per-row rule (ca_score_select: softmax over causal key blocks,
+     keep score > threshold, sink and local blocks);
+  5. Q-block and GQA union into per-KV-group tables (ca_union_compact);
+  6. indexed attention over the cache pages (ca_attn_fwd).
+Steps 2-5 replace the reference's _compute_chunked_gate_from_cache + AttnGate +
+chunked_prefill_column_dense_attention_forward; their bits are pinned by the kernel tests
+against the CPU oracle.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+from torch import nn
+
+from ... import ops
+from ...modules._core import COMPACTATTN_VERSION
+from ..attn_gate import AttnGate
+from .configuration_llama_seerattn import SeerAttnLlamaConfig
+from .modeling_llama_common import ChunkedPrefillCache, CompactAttnLlamaForCausalLM, apply_rotary_pos_emb
+
+BLOCK = 64
+
+
+class LlamaSeerAttentionChunkedDense(nn.Module):
+    def __init__(self, config: SeerAttnLlamaConfig, layer_idx: int, device=None):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.head_dim = config.head_dim
+        self.num_heads = config.num_attention_heads
+        self.num_key_value_heads = config.num_key_value_heads
+        self.num_key_value_groups = config.num_key_value_groups
+        self.scaling = self.head_dim ** -0.5
+        kw = dict(bias=False, device=device, dtype=torch.bfloat16)
+        self.q_proj = nn.Linear(config.hidden_size, self.num_heads * self.head_dim, **kw)
+        self.k_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
+        self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
+        self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
+        self.attn_gate = AttnGate(config.seerattn_gate_block_size, self.head_dim, config.seerattn_gate_hidden_size,
+                                  self.num_key_value_heads, self.num_heads,
+                                  force_double=config.seerattn_gate_force_double).to(device)
+        self.compactattn_keep_recent_blocks = config.seerattn_compactattn_keep_recent_blocks
+        self.compactattn_version = COMPACTATTN_VERSION
+        self.compactattn_debug = False
+        self._compactattn_last_stats = None
+
+    def _selection_rule(self) -> ops.Rule:
+        c = self.config
+        return ops.Rule(threshold=float(c.seerattn_threshold), sink_blocks=c.compactattn_sink_blocks,
+                        local_blocks=c.compactattn_local_blocks)
+
+    def _append_compactattn_chunked_gate_key_cache(self, key_states_nope: torch.Tensor, cache, past: int,
+                                                   block_position_embeddings) -> None:
+        cos, sin = block_position_embeddings
+        B = key_states_nope.shape[0]
+        ops.cache_fill(key_states_nope, None, None, None, [past] * B, cache.cap, None,
+                       gate_wk=self.attn_gate.mask_linear_k.weight.detach(), rope_cos=cos, rope_sin=sin,
+                       kgate=cache.kgate)
+
+    def _select_tables(self, query_states_nope: torch.Tensor, cache, past: int, block_position_embeddings
+                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+        cos, sin = block_position_embeddings
+        B = query_states_nope.shape[0]
+        P = [past] * B
+        qhat = ops.pool_query(query_states_nope, P, cache.cap,
+                              gate_wq=self.attn_gate.mask_linear_q.weight.detach(), rope_cos=cos, rope_sin=sin,
+                              num_kv_heads=self.num_key_value_heads)
+        rowmask, _ = ops.score_select(qhat, cache.kgate, self.attn_gate.scale, self._selection_rule(), P,
+                                      self.num_key_value_heads, cache.cap)
+        table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap)
+        return table, counts
+
+    def _do_chunked_compactattn_attention(self, query_states: torch.Tensor, query_states_nope: torch.Tensor, cache,
+                                          past: int, block_position_embeddings, dense: bool):
+        B, L = query_states.shape[:2]
+        P = [past] * B
+        if dense:
+            table, counts = ops.dense_table(P, L, self.num_heads, self.num_key_value_heads, cache.cap,
+                                            query_states.device)
+        else:
+            table, counts = self._select_tables(query_states_nope, cache, past, block_position_embeddings)
+        K, V = cache.layouts()
+        out = ops.attn_fwd(query_states, K, V, table, counts, P, self.scaling, cache.cap, self.num_key_value_heads)
+        return out, table, counts
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings: Tuple[torch.Tensor, torch.Tensor],
+                attention_mask: Optional[torch.Tensor] = None, past_key_value: Optional[ChunkedPrefillCache] = None,
+                cache_position: Optional[torch.LongTensor] = None,
+                block_position_embeddings: Optional[Tuple[torch.Tensor, torch.Tensor]] = None, **kwargs):
+        del cache_position, kwargs
+        if past_key_value is None:
+            raise ValueError("the compactattn prefill path needs a ChunkedPrefillCache")
+        if attention_mask is not None and not bool(attention_mask.all()):
+            raise ValueError("padded positions are not supported by the compactattn prefill path")
+        if block_position_embeddings is None:
+            raise ValueError("block_position_embeddings (per-block rotary tables) are required")
+        B, L, _ = hidden_states.shape
+        if L % BLOCK:
+            raise ValueError("chunk lengths must be multiples of 64 tokens")
+        q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim)
+        k = self.k_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
+        v = self.v_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
+        cos, sin = position_embeddings
+        query_states, key_states = apply_rotary_pos_emb(q, k, cos, sin)
+
+        cache = past_key_value.layer(self.layer_idx)
+        past = cache.append(key_states, v.contiguous())
+        self._append_compactattn_chunked_gate_key_cache(k.contiguous(), cache, past, block_position_embeddings)
+        dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
+        out, table, counts = self._do_chunked_compactattn_attention(query_states, q.contiguous(), cache, past,
+                                                                   block_position_embeddings, dense)
+        out = self.o_proj(out.reshape(B, L, -1))
+        if self.compactattn_debug:
+            self._compactattn_last_stats = {
+                "path": "first_chunk_dense" if past == 0 else ("forced_dense" if dense else "chunked_selected"),
+                "past_blocks": past, "table": table, "counts": counts,
+                "compactattn_version": self.compactattn_version,
+            }
+        else:
+            self._compactattn_last_stats = None
+        return out, 0.0, None, None, None
+
+
+class SeerAttnLlamaChunkedDenseForCausalLM(CompactAttnLlamaForCausalLM):
+    attn_cls = LlamaSeerAttentionChunkedDense
+    cache_with_kgate = True

@@ -1,0 +1,187 @@
+"""GPU tests of the compactattn Llama models (chunked prefill through the HIP kernels).
+
+- dense chunked prefill (every chunk over the whole past) matches an fp32 CPU forward of
+  the same weights;
+- a Seer threshold below every score keeps every block, so its logits equal the dense
+  run's bit for bit (the tables are the identity);
+- for one layer and chunk, the tables the model builds equal the CPU oracle's (bit-exact)
+  for both selectors, recomputed from the layer's own Q/K, and the layer's attention output
+  is within the north-star tolerance of the oracle over those tables.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import oracle
+from compactattention_amd.chunked_prefill import run_chunked_prefill_once, synthetic_prompt
+from compactattention_amd.prefill_sparse.llama import (SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaConfig,
+                                                       SeerAttnLlamaFlashPrefillCompactAttnForCausalLM)
+from compactattention_amd.prefill_sparse.llama.modeling_llama_common import apply_rotary_pos_emb
+
+from .util import bits, f32
+
+pytestmark = pytest.mark.gpu
+
+T, CHUNK = 1280, 256
+
+
+def tiny_config(**kw) -> SeerAttnLlamaConfig:
+    base = dict(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                num_key_value_heads=2, max_position_embeddings=2048, seerattn_threshold=0.02,
+                seerattn_flashprefill_alpha=0.3)
+    base.update(kw)
+    return SeerAttnLlamaConfig(**base)
+
+
+def _model(cls, gpu, qk_scale: float = 1.0, gate_scale: float = 1.0, **kw):
+    m = cls(tiny_config(**kw), device=gpu)
+    m.init_weights(seed=11)
+    # larger projections than N(0, 0.02) give the tiny model selective (non-flat) block scores
+    with torch.no_grad():
+        for layer in m.model.layers:
+            layer.self_attn.q_proj.weight.mul_(qk_scale)
+            layer.self_attn.k_proj.weight.mul_(qk_scale)
+            if hasattr(layer.self_attn, "attn_gate"):
+                layer.self_attn.attn_gate.mask_linear_q.weight.mul_(gate_scale)
+                layer.self_attn.attn_gate.mask_linear_k.weight.mul_(gate_scale)
+    return m
+
+
+def _reference_logits(model, input_ids: torch.Tensor) -> torch.Tensor:
+    """fp32 CPU forward over the whole prompt with causal softmax attention."""
+    c = model.config
+    sd = {k: v.detach().float().cpu() for k, v in model.state_dict().items()}
+    ids = input_ids.cpu()
+    h = sd["model.embed_tokens.weight"][ids]
+    L = ids.shape[1]
+    cos = model.model.rotary_emb.cos[:L].cpu()
+    sin = model.model.rotary_emb.sin[:L].cpu()
+
+    def rms(x, w):
+        return w * F.rms_norm(x, (x.shape[-1],), eps=c.rms_norm_eps)
+
+    for i in range(c.num_hidden_layers):
+        p = f"model.layers.{i}."
+        x = rms(h, sd[p + "input_layernorm.weight"])
+        q = (x @ sd[p + "self_attn.q_proj.weight"].T).view(1, L, c.num_attention_heads, 128)
+        k = (x @ sd[p + "self_attn.k_proj.weight"].T).view(1, L, c.num_key_value_heads, 128)
+        v = (x @ sd[p + "self_attn.v_proj.weight"].T).view(1, L, c.num_key_value_heads, 128)
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        g = c.num_key_value_groups
+        kq = k.repeat_interleave(g, dim=2)
+        vq = v.repeat_interleave(g, dim=2)
+        s = torch.einsum("bqhd,bkhd->bhqk", q, kq) / math.sqrt(128)
+        s = s.masked_fill(torch.ones(L, L, dtype=torch.bool).triu(1), float("-inf"))
+        o = torch.einsum("bhqk,bkhd->bqhd", torch.softmax(s, -1), vq).reshape(1, L, -1)
+        h = h + o @ sd[p + "self_attn.o_proj.weight"].T
+        x = rms(h, sd[p + "post_attention_layernorm.weight"])
+        mlp = F.silu(x @ sd[p + "mlp.gate_proj.weight"].T) * (x @ sd[p + "mlp.up_proj.weight"].T)
+        h = h + mlp @ sd[p + "mlp.down_proj.weight"].T
+    h = rms(h, sd["model.norm.weight"])
+    return h[:, -1:] @ sd["lm_head.weight"].T
+
+
+def test_dense_prefill_matches_fp32_reference(gpu):
+    print("case: model dense vs fp32", flush=True)
+    m = _model(SeerAttnLlamaChunkedDenseForCausalLM, gpu, seerattn_chunked_prefill_force_dense=True)
+    ids = synthetic_prompt(1, T, m.config.vocab_size, 1234, gpu)
+    logits, _ = run_chunked_prefill_once(m, ids, CHUNK)
+    ref = _reference_logits(m, ids)
+    got = logits.float().cpu()
+    cos = F.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item()
+    assert cos > 0.999, cos
+    assert (got - ref).abs().max().item() <= 0.05 * ref.abs().max().item()
+
+
+def test_seer_keep_all_equals_dense(gpu):
+    print("case: model keep-all vs dense", flush=True)
+    ids = synthetic_prompt(1, T, 512, 99, gpu)
+    dense = _model(SeerAttnLlamaChunkedDenseForCausalLM, gpu, seerattn_chunked_prefill_force_dense=True)
+    keep_all = _model(SeerAttnLlamaChunkedDenseForCausalLM, gpu, seerattn_threshold=-1.0)
+    a, _ = run_chunked_prefill_once(dense, ids, CHUNK)
+    b, _ = run_chunked_prefill_once(keep_all, ids, CHUNK)
+    assert torch.equal(a, b)
+
+
+def _capture_layer_inputs(model, layer_idx):
+    captured = []
+    attn = model.model.layers[layer_idx].self_attn
+    handle = attn.register_forward_pre_hook(lambda mod, args: captured.append(args[0].detach().clone()))
+    attn.compactattn_debug = True
+    return captured, handle, attn
+
+
+def _layer_qkv(attn, hidden, start, model):
+    B, L, _ = hidden.shape
+    q = attn.q_proj(hidden).view(B, L, attn.num_heads, 128)
+    k = attn.k_proj(hidden).view(B, L, attn.num_key_value_heads, 128)
+    v = attn.v_proj(hidden).view(B, L, attn.num_key_value_heads, 128)
+    cos, sin = model.model.rotary_emb.tokens(start, L)
+    qr, kr = apply_rotary_pos_emb(q, k, cos, sin)
+    return q, k, v, qr, kr
+
+
+@pytest.mark.parametrize("selector", ["seer", "flashprefill"])
+def test_layer_tables_bit_exact(gpu, selector):
+    print(f"case: model layer tables {selector}", flush=True)
+    cls = SeerAttnLlamaChunkedDenseForCausalLM if selector == "seer" else SeerAttnLlamaFlashPrefillCompactAttnForCausalLM
+    m = _model(cls, gpu, qk_scale=8.0 if selector == "seer" else 40.0, gate_scale=20.0, seerattn_threshold=0.1)
+    layer_idx = 1
+    captured, handle, attn = _capture_layer_inputs(m, layer_idx)
+    ids = synthetic_prompt(1, T, m.config.vocab_size, 7, gpu)
+    with torch.no_grad():
+        run_chunked_prefill_once(m, ids, CHUNK)
+    handle.remove()
+    stats = attn._compactattn_last_stats
+    assert stats["past_blocks"] == (T - CHUNK) // 64
+    with torch.no_grad():
+        parts = [_layer_qkv(attn, h, i * CHUNK, m) for i, h in enumerate(captured)]
+    q_nope, k_nope, _, q_rope, _ = parts[-1]
+    k_nope_all = torch.cat([p[1] for p in parts], dim=1)
+    k_rope_all = torch.cat([p[4] for p in parts], dim=1)
+    v_all = torch.cat([p[2] for p in parts], dim=1)
+    P = [stats["past_blocks"]]
+    Hkv = m.config.num_key_value_heads
+    c = m.config
+    if selector == "seer":
+        bcos, bsin = (f32(t) for t in m.model.rotary_emb.blocks())
+        wq = f32(attn.attn_gate.mask_linear_q.weight)
+        wk = f32(attn.attn_gate.mask_linear_k.weight)
+        qhat = oracle.gate_project(oracle.block_mean(bits(q_nope)), wq, bcos, bsin, P)
+        khat = oracle.gate_project(oracle.block_mean(bits(k_nope_all)), wk, bcos, bsin, [0])
+        scores = oracle.block_scores(qhat, khat, P, 128 ** -0.5)
+        rule = oracle.Rule(threshold=c.seerattn_threshold, sink_blocks=c.compactattn_sink_blocks,
+                           local_blocks=c.compactattn_local_blocks)
+        last_n = 0
+    else:
+        qhat = oracle.block_mean(bits(q_rope))
+        khat = oracle.block_mean(bits(k_rope_all))
+        scores = oracle.block_scores(qhat, khat, P, 1.0 / math.sqrt(128))
+        rule = oracle.Rule(topk=c.seerattn_flashprefill_min_budget, alpha=c.seerattn_flashprefill_alpha,
+                           sink_blocks=c.seerattn_flashprefill_attention_sink,
+                           window_blocks=c.seerattn_flashprefill_window_size,
+                           last_n_block=c.seerattn_flashprefill_last_n_block)
+        last_n = c.seerattn_flashprefill_last_n_block
+    keep = oracle.select_rows(scores, P, rule)
+    _, _, table, counts = oracle.union_compact(keep, Hkv, P, last_n)
+    got_counts = stats["counts"].cpu().numpy()
+    got_table = stats["table"].cpu().numpy()
+    assert np.array_equal(got_counts, counts)
+    assert np.array_equal(got_table, table)
+    nkb = P[0] + CHUNK // 64
+    assert counts.min() < nkb, "the test wants a selective layer (some blocks dropped)"
+    # attention over the selected pages, recomputed from the layer's own inputs
+    kc = k_rope_all.transpose(1, 2).contiguous()
+    vc = v_all.transpose(1, 2).contiguous()
+    ref = oracle.attention(bits(q_rope), bits(kc), bits(vc), P, table, counts, 128 ** -0.5)
+    out = torch.empty_like(q_rope)
+    from compactattention_amd import ops
+    ops.attn_fwd(q_rope, ops.KV.heads_first(kc), ops.KV.heads_first(vc), stats["table"], stats["counts"], P,
+                 128 ** -0.5, kc.shape[2] // 64, Hkv, out=out)
+    err = np.abs(f32(out) - ref)
+    assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())

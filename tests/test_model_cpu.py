@@ -1,0 +1,81 @@
+"""CPU checks of the compactattn model integration: configuration, construction, seeded
+initialisation and argument errors (no kernel runs without a GPU)."""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from compactattention_amd.chunked_prefill import synthetic_prompt
+from compactattention_amd.prefill_sparse.llama import (SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaConfig,
+                                                       SeerAttnLlamaFlashPrefillCompactAttnForCausalLM)
+from compactattention_amd.prefill_sparse.llama.modeling_llama_common import apply_rotary_pos_emb, rotate_half
+
+
+def tiny(**kw):
+    base = dict(vocab_size=64, hidden_size=128, intermediate_size=256, num_hidden_layers=2, num_attention_heads=2,
+                num_key_value_heads=1, max_position_embeddings=512)
+    base.update(kw)
+    return SeerAttnLlamaConfig(**base)
+
+
+def test_default_config_is_llama_8b_shape():
+    c = SeerAttnLlamaConfig()
+    assert (c.hidden_size, c.num_hidden_layers, c.num_attention_heads, c.num_key_value_heads) == (4096, 32, 32, 8)
+    assert (c.intermediate_size, c.vocab_size, c.rope_theta) == (14336, 128256, 500000.0)
+    assert c.num_key_value_groups == 4
+    c.validate()
+
+
+def test_config_validation():
+    with pytest.raises(ValueError, match="unknown config fields"):
+        SeerAttnLlamaConfig.from_dict({"hidden_size": 8, "nope": 1})
+    with pytest.raises(ValueError, match="64-token blocks"):
+        tiny(seerattn_gate_block_size=128).validate()
+    with pytest.raises(ValueError, match="head_dim 128"):
+        tiny(head_dim=64).validate()
+    with pytest.raises(ValueError, match="Qavg_Kavg"):
+        tiny(seerattn_gate_type="Qmax_Kmax").validate()
+    assert SeerAttnLlamaConfig.from_dict(tiny().to_dict()) == tiny()
+
+
+@pytest.mark.parametrize("cls", [SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaFlashPrefillCompactAttnForCausalLM])
+def test_construction_and_seeded_init(cls):
+    a = cls(tiny())
+    b = cls(tiny())
+    a.init_weights(seed=5)
+    b.init_weights(seed=5)
+    for (na, pa), (nb, pb) in zip(a.named_parameters(), b.named_parameters()):
+        assert na == nb and torch.equal(pa, pb)
+    assert torch.all(a.model.norm.weight == 1)
+    assert a.lm_head.weight.dtype == torch.bfloat16
+    names = {n for n, _ in a.named_parameters()}
+    assert "model.layers.0.self_attn.q_proj.weight" in names
+    if cls is SeerAttnLlamaChunkedDenseForCausalLM:
+        assert a.model.layers[0].self_attn.attn_gate.mask_linear_q.weight.shape == (2, 128, 128)
+
+
+def test_rope_matches_rotate_half_formula():
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn((1, 8, 2, 128), generator=g)
+    k = torch.randn((1, 8, 1, 128), generator=g)
+    m = SeerAttnLlamaChunkedDenseForCausalLM(tiny())
+    cos, sin = m.model.rotary_emb.tokens(3, 8)
+    qr, kr = apply_rotary_pos_emb(q, k, cos, sin)
+    # the rotation keeps each (i, i + 64) pair's norm and is the identity at position 0
+    pair = lambda x: x[..., :64] ** 2 + x[..., 64:] ** 2  # noqa: E731
+    assert torch.allclose(pair(qr), pair(q), atol=1e-5)
+    c0, s0 = m.model.rotary_emb.tokens(0, 1)
+    assert torch.allclose(apply_rotary_pos_emb(q[:, :1], k[:, :1], c0, s0)[0], q[:, :1])
+    assert torch.equal(rotate_half(rotate_half(q)), -q)
+    bc, bs = m.model.rotary_emb.blocks()
+    assert torch.equal(bc[2], m.model.rotary_emb.cos[128])
+
+
+def test_forward_rejects_decode_and_cpu():
+    m = SeerAttnLlamaChunkedDenseForCausalLM(tiny())
+    ids = synthetic_prompt(1, 128, 64, 0, "cpu")
+    with pytest.raises(ValueError, match="decode"):
+        m(ids[:, :1], None)
+    cache = m.new_cache(1, 128)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        m(ids, cache)
