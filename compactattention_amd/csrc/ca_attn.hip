@@ -10,19 +10,22 @@
 // Work decomposition
 //  - The G query heads of a KV group share the group's block table, so a KV row
 //    (request, kv head) owns Lq*G "packed" query rows r = t*G + g (token t, head g).
-//  - A workgroup (4 waves) takes 128 packed rows; each wave keeps 32 rows (one 32x32 MFMA
-//    tile) for the whole KV loop: Q in VGPRs, O^T in accumulators.  Two workgroups share a
-//    CU, so each SIMD runs two waves whose softmax and MFMA phases overlap.
+//  - A workgroup (8 waves, one per CU) takes 256 packed rows; each wave keeps 32 rows (one
+//    32x32 MFMA tile) for the whole KV loop: Q in VGPRs, O^T in accumulators.  Each SIMD
+//    runs two waves whose softmax and MFMA phases overlap; a wave raises its issue
+//    priority while it feeds the S^T MFMAs.
 //  - Scores are computed transposed, S^T = K Q^T (A = K from LDS, B = Q from VGPRs), so the
 //    softmax output lands in exactly the VGPR layout the second product's B operand needs:
 //    O^T += V^T P^T (A = V^T from LDS).  Inside each 32-key S^T tile the A-row -> key map
 //    swaps bits 2 and 3 of the row index, which makes every lane's 8 P values 8 consecutive
-//    keys, i.e. one 16-byte V^T read.
-//  - K blocks are stored in LDS row-major with a 272-byte row pitch (conflict-free fragment
-//    reads at immediate offsets); V blocks are transposed on their way into LDS (register
-//    8x4 transpose) into V^T rows with 16-byte chunks XOR-swizzled by row.
-//  - Two LDS stages: the next block's global loads are in flight while the current block is
-//    computed.  Optional split of each row's block list (split-KV) with an LSE merge.
+//    keys.
+//  - K and V blocks go from HBM to LDS by LDS-DMA buffer loads (no staging registers),
+//    row-major with XOR swizzles that keep the fragment reads free of bank conflicts.  V^T
+//    fragments are read with the gfx950 transposing LDS read (ds_read_b64_tr_b16), two
+//    per MFMA.
+//  - Four LDS stages: the DMA of the next three blocks is in flight while the current
+//    block is computed, and a step waits only for the block after it.  Optional split of
+//    each row's block list (split-KV) with an LSE merge.
 //  - Workgroup ids are remapped so consecutive work items (same KV row) share an XCD and
 //    its L2.
 
@@ -40,13 +43,15 @@ typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
-constexpr int kNW = 4;               // waves per workgroup (32 packed query rows each)
+constexpr int kNW = 8;     // waves per workgroup (32 packed query rows each)
+constexpr int kStages = 4;  // LDS stages (K + V of one block each): 128 KB per workgroup
 constexpr int kBM = 32 * kNW;        // packed query rows per workgroup
-constexpr int kKPitch = 272;  // bytes per K row in LDS (256 + 16 pad: conflict-free fragment reads)
-constexpr int kVPitch = 128;  // bytes per V^T row in LDS (16-byte chunks XOR-swizzled by row)
-constexpr int kKBytes = 64 * kKPitch;
-constexpr int kVBytes = 128 * kVPitch;
+constexpr int kKBytes = 64 * 256;  // K rows of one block in LDS (swizzled, unpadded)
+constexpr int kVBytes = 64 * 256;  // V rows of one block in LDS (swizzled, unpadded)
 constexpr int kStageBytes = kKBytes + kVBytes;
 constexpr float kRescale = 8.0f;      // lazy-rescale slack (log2 units)
 
@@ -74,22 +79,26 @@ __device__ __forceinline__ int swap23(int m) {
     return (m & ~12) | ((m & 4) << 1) | ((m & 8) >> 1);
 }
 
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) {
-    return (a & 0xffffu) | (b << 16);
+__device__ __forceinline__ lds_void_t* to_lds(const uint8_t* p) {
+    return (lds_void_t*)(p);
 }
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) {
-    return (a >> 16) | (b & 0xffff0000u);
+__device__ __forceinline__ lds_i16x4_t* to_lds_v4(const uint8_t* p) {
+    return (lds_i16x4_t*)(p);
+}
+// Completes this wave's outstanding LDS-DMA loads (vector-memory counter).
+__device__ __forceinline__ void wait_dma() {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 
 // NW waves per workgroup, 32 packed query rows per wave (one 32x32 MFMA row tile), so a
 // workgroup owns BM = 32*NW rows.  Registers stay within 256 per lane, which lets two waves
-// share a SIMD: one wave's softmax overlaps the other's MFMAs.
+// share a SIMD: one wave's softmax overlaps the other's MFMAs.  One 8-wave workgroup per
+// CU (128 KB of LDS).
 template <int NW>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fwd_kernel(AttnParams p) {
     constexpr int BM = 32 * NW;
-    constexpr int NT = NW * 64;
-    __shared__ __attribute__((aligned(16))) uint8_t smem[2][kStageBytes];  // [stage]: K rows, then V^T rows
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kStages * kStageBytes];  // [stage]: K rows, then V rows
 
     const int L = blockIdx.x;
     const int W = (L & 7) * p.per_xcd + (L >> 3);
@@ -163,67 +172,37 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int32_t* kpt = p.k.page_table ? p.k.page_table + (int64_t)row * p.k.pts : nullptr;
     const int32_t* vpt = p.v.page_table ? p.v.page_table + (int64_t)row * p.v.pts : nullptr;
 
-    // ---- global -> LDS staging of one block ----
-    // With 256 threads every thread moves 4 x 16 B of K and 8 x 8 B of V; with 512 threads
-    // the first half moves K and the second half V.  32-bit element offsets inside a block
-    // (the host checks 64 * stride_tok < 2^30) on top of a wave-uniform block base.
-    constexpr bool kSplitKV = NT >= 512;
-    const int kt_id = kSplitKV ? (tid & 255) : tid;
-    const bool does_k = !kSplitKV || tid < 256;
-    const bool does_v = !kSplitKV || tid >= 256;
-    const int k_key0 = kt_id >> 4;  // + 16*i
-    const int k_chunk = kt_id & 15;
-    const int v_kg = kt_id >> 5;
-    const int v_dg = kt_id & 31;
-    // Loads go through buffer resources built per block (wave-uniform base in SGPRs), so a
-    // lane needs one 32-bit offset register per tensor; the per-row/per-key strides ride in
-    // the scalar offset.
+    // ---- global -> LDS staging of one block (LDS DMA) ----
+    // A block is 64 K rows and 64 V rows of 256 bytes.  Each wave issues 2 + 2 buffer loads
+    // that write LDS directly (1 KB per instruction: lane L fills bytes 16L..16L+15 of the
+    // instruction's 4 rows); the lane chooses which global 16-byte chunk lands there, which
+    // applies the XOR swizzles.  Wave w moves rows 4w + 32i + L/16 (i = 0, 1), so a lane's
+    // swizzle is the same for its two rows:
+    //   K: 16-byte chunk c of row r sits at chunk c ^ (r & 15)    (conflict-free b128 reads)
+    //   V: 16-byte chunk c of row r sits at chunk c ^ 4 (r & 3)   (conflict-free transposed reads)
+    // 32-bit offsets inside a block (the host checks 64 * stride_tok < 2^30) on top of a
+    // wave-uniform block base in the buffer resource.
+    static_assert(NW == 8, "the staging split assumes eight waves");
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    const int st_row = 4 * wu + (l >> 4);
     const int kstok_b = static_cast<int>(p.k.stok) * 2;
     const int vstok_b = static_cast<int>(p.v.stok) * 2;
-    const int k_voff = k_key0 * kstok_b + 16 * k_chunk;
-    const int v_voff = 8 * v_kg * vstok_b + 8 * v_dg;
-    u32x4_t kreg[4];
-    u32x2_t vreg[8];
-    auto load_block = [&](int e) {
+    const int k_goff = st_row * kstok_b + (((l & 15) ^ (st_row & 15)) * 16);
+    const int v_goff = st_row * vstok_b + (((l & 15) ^ (4 * (st_row & 3))) * 16);
+    auto issue_block = [&](int e, int stage) {
         const int kb = block_id(e);
-        if (does_k) {
-            const int64_t kphys = kpt ? kpt[kb] : kb;
-            const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(kbase_row + kphys * p.k.sblk), 0, 0x7fffffff, 0x00020000);
+        const int64_t kphys = kpt ? kpt[kb] : kb;
+        const int64_t vphys = vpt ? vpt[kb] : kb;
+        const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(kbase_row + kphys * p.k.sblk), 0, 0x7fffffff, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<uint16_t*>(vbase_row + vphys * p.v.sblk), 0, 0x7fffffff, 0x00020000);
+        uint8_t* kdst = smem + stage * kStageBytes + wu * 1024;
+        uint8_t* vdst = kdst + kKBytes;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rk, k_voff, i * 16 * kstok_b, 0);
-        }
-        if (does_v) {
-            const int64_t vphys = vpt ? vpt[kb] : kb;
-            const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-                const_cast<uint16_t*>(vbase_row + vphys * p.v.sblk), 0, 0x7fffffff, 0x00020000);
-#pragma unroll
-            for (int r = 0; r < 8; ++r) vreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rv, v_voff, r * vstok_b, 0);
-        }
-    };
-    auto store_block = [&](int stage) {
-        if (does_k) {
-            uint8_t* ks = smem[stage];
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<u32x4_t*>(ks + (k_key0 + 16 * i) * kKPitch + k_chunk * 16) = kreg[i];
-        }
-        if (does_v) {
-            uint8_t* vs = smem[stage] + kKBytes;
-            // transpose 8 keys x 4 d into 4 rows of V^T (8 keys each)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                u32x4_t o;
-#pragma unroll
-                for (int q2 = 0; q2 < 4; ++q2) {
-                    const uint32_t a = (j < 2) ? vreg[2 * q2].x : vreg[2 * q2].y;
-                    const uint32_t c = (j < 2) ? vreg[2 * q2 + 1].x : vreg[2 * q2 + 1].y;
-                    o[q2] = (j & 1) ? pack_hi(a, c) : pack_lo(a, c);
-                }
-                const int d = 4 * v_dg + j;
-                *reinterpret_cast<u32x4_t*>(vs + d * kVPitch + ((v_kg ^ ((d >> 1) & 7)) * 16)) = o;
-            }
+        for (int i = 0; i < 2; ++i) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, to_lds(kdst + i * 8192), 16, k_goff, i * 32 * kstok_b, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, to_lds(vdst + i * 8192), 16, v_goff, i * 32 * vstok_b, 0, 0);
         }
     };
 
@@ -233,25 +212,38 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // O^T += V^T P^T (16 MFMAs).  m_run only rises when a row's scaled block max exceeds it
     // by more than kRescale (log2 units); otherwise P = exp2(s - m_run) < 2^kRescale and the
     // accumulators keep their scale.
-    // Fragment addresses: lane-constant bases, per-fragment offsets are immediates.
-    const int k_lane = swap23(n) * kKPitch + h * 16;
-    const int v_lane = n * kVPitch;
+    // Fragment addresses.  K (A operand of S^T): lane row swap23(n) (+32 per 32-key half),
+    // 16 bytes at d = 16 ds + 8 h.  V^T (A operand of O^T): each transposed b64 read gives
+    // a lane 4 keys of one d column: lane l reads the 8 bytes at row 16 s4 + 8 h + 4 hh +
+    // (l & 15) / 4, d = 32 dt + 16 ((l >> 4) & 1) + 4 (l & 3), which hands it keys
+    // 16 s4 + 8 h + 4 hh + i (i = 0..3) of column d = 32 dt + n.  s4 and hh are immediates.
+    const int k_r = swap23(n);
+    int k_off[8];
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) k_off[ds] = k_r * 256 + (((2 * ds + h) ^ (k_r & 15)) * 16);
+    const int v_rq = (l & 15) >> 2;
+    const int v_x = 2 * ((l >> 4) & 1) + ((l & 3) >> 1);
+    int v_off[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) v_off[dt] = (8 * h + v_rq) * 256 + (4 * (dt ^ v_rq) + v_x) * 16 + (l & 1) * 8;
     auto process = [&](int kb, const uint8_t* stage_base, bool masked) {
-        const uint8_t* ks = stage_base + k_lane;
-        const uint8_t* vs = stage_base + kKBytes + v_lane;
+        const uint8_t* ks = stage_base;
+        const uint8_t* vs = stage_base + kKBytes;
         f32x16_t sacc[2];
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.0f;
         // the two 32-key accumulators alternate so consecutive MFMAs are independent
+        __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int ds = 0; ds < 8; ++ds)
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + kt * 32 * kKPitch + ds * 32);
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + k_off[ds] + kt * 8192);
                 sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ds], sacc[kt], 0, 0, 0);
             }
+        __builtin_amdgcn_s_setprio(0);
         if (masked) {
             // value j of half kt holds key kt*32 + swap23(8*(j/4) + 4*h + j%4)
             // = kt*32 + 8*h + key_off(j); visible iff kb*64 + key <= 64*P + t
@@ -304,30 +296,35 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int s4 = 0; s4 < 4; ++s4) {
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(vs + dt * 32 * kVPitch + (((2 * s4 + h) ^ ((n >> 1) & 7)) * 16));
+                const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(to_lds_v4(vs + v_off[dt] + s4 * 4096));
+                const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(to_lds_v4(vs + v_off[dt] + s4 * 4096 + 1024));
+                const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
                 oacc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf[s4], oacc[dt], 0, 0, 0);
             }
         }
     };
 
-    // ---- KV loop: two LDS stages, next block's global loads in flight during compute ----
-    if (e0 < e1) {
-        load_block(e0);
-        store_block(0);
-        __syncthreads();
-    }
-    auto step = [&](int e, bool masked) {
-        const int stage = (e - e0) & 1;
-        const bool has_next = e + 1 < e1;
-        if (has_next) load_block(e + 1);
-        process(block_id(e), smem[stage], masked);
-        if (has_next) store_block(stage ^ 1);
+    // ---- KV loop: four LDS stages, DMA three blocks ahead ----
+    const int nblk = e1 - e0;
+    for (int i = 0; i < 3; ++i)
+        if (i < nblk) issue_block(e0 + i, i);
+    // block 0 must have landed (4 loads per block and wave)
+    if (nblk > 2) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (nblk > 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else wait_dma();
+    __syncthreads();
+    auto step = [&](int idx, bool masked) {
+        if (idx + 3 < nblk) issue_block(e0 + idx + 3, (idx + 3) % kStages);
+        process(block_id(e0 + idx), smem + (idx % kStages) * kStageBytes, masked);
+        // block idx+1 must have landed; later blocks may stay in flight
+        if (idx + 3 < nblk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else if (idx + 2 < nblk) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+        else wait_dma();
         __syncthreads();
     };
-    int e = e0;
-    for (; e < e_mask; ++e) step(e, false);
-    for (; e < e1; ++e) step(e, true);
-    (void)kt_id;
+    int idx = 0;
+    for (; idx < e_mask - e0; ++idx) step(idx, false);
+    for (; idx < nblk; ++idx) step(idx, true);
 
     // ---- epilogue ----
     // lanes n and n + 32 hold different keys of the same row: their partial sums combine
@@ -415,14 +412,14 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 }  // namespace
 
 int attn_pick_splits(const Shape& s, const PastBlocks& pb) {
-    // Two workgroups are resident per CU (70 KB LDS and <= 256 registers per lane each).  A
-    // launch wants about two rounds of them (4 x 256 workgroups) to even out the per-tile
-    // work differences, so the block lists are split when the work items alone do not reach
-    // that, keeping at least ~16 blocks per split.
+    // One workgroup is resident per CU (128 KB of LDS).  A launch wants about two rounds of
+    // them (2 x 256 workgroups) to even out the per-tile work differences, so the block
+    // lists are split when the work items alone do not reach that, keeping at least ~16
+    // blocks per split.
     const int rows_total = s.Lq * s.G;
     const int ntiles = (rows_total + kBM - 1) / kBM;
     const int items = s.B * s.Hkv * ntiles;
-    constexpr int kSlots = 4 * 256;  // two resident rounds: smooths the per-tile work imbalance
+    constexpr int kSlots = 2 * 256;  // two resident rounds: smooths the per-tile work imbalance
     int max_blocks = 0;
     for (int b = 0; b < s.B; ++b) max_blocks = max(max_blocks, pb.p[b] + s.Qb);
     int splits = items >= kSlots ? 1 : (kSlots + items / 2) / items;
