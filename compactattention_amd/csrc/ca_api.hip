@@ -310,9 +310,9 @@ int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout*
     if (table_stride < a.s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, a.s.cap);
     if (!(scale > 0.0f)) return fail(CA_ERR_INVALID, "scale must be positive");
     if ((int64_t)a.s.Lq * a.s.G > (int64_t)1 << 24) return fail(CA_ERR_LIMIT, "q_len * group too large");
-    if (num_splits == 0) num_splits = ca::attn_pick_splits(a.s, a.pb);
-    if (num_splits < 1 || num_splits > 16) return fail(CA_ERR_INVALID, "num_splits=%d outside [1, 16]", num_splits);
-    const int64_t need = ca::attn_workspace_bytes(a.s, num_splits);
+    if (num_splits < 0 || num_splits > 16) return fail(CA_ERR_INVALID, "num_splits=%d outside [0, 16]", num_splits);
+    const int max_splits = num_splits == 0 ? ca::attn_pick_splits(a.s, a.pb) : num_splits;
+    const int64_t need = ca::attn_workspace_bytes(a.s, max_splits);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
         return fail(CA_ERR_WORKSPACE, "num_splits=%d needs a 16-byte aligned workspace of %lld bytes (got %lld)",
                     num_splits, (long long)need, (long long)workspace_bytes);

@@ -66,13 +66,17 @@ struct AttnParams {
     float scale_log2;  // softmax scale * log2(e)
     SeqAddr out;
     float* lse;
-    int splits;
     int ntiles;       // packed-row tiles per KV row
     int rows_total;   // Lq * G
     int total_items;  // B*Hkv*ntiles*splits
     int per_xcd;      // ceil(total_items / 8)
-    float* ws_o;      // [splits][B*Hkv][rows_total][128]
-    float* ws_lse;    // [splits][B*Hkv][rows_total]  (log2 domain)
+    float* ws_o;      // [max splits][B*Hkv][rows_total][128]
+    float* ws_lse;    // [max splits][B*Hkv][rows_total]  (log2 domain)
+    int32_t sp[CA_MAX_BATCH];        // splits of each request's block lists
+    int32_t ioff[CA_MAX_BATCH + 1];  // first work item of each request (linear placement)
+    int use_rows;                    // rows placed per XCD (xrow / xoff)
+    int32_t xoff[9];
+    uint16_t xrow[kPlanRows];
 };
 
 __device__ __forceinline__ int swap23(int m) {
@@ -100,16 +104,37 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     constexpr int BM = 32 * NW;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kStages * kStageBytes];  // [stage]: K rows, then V rows
 
+    // workgroup -> (XCD x, k-th work item of x) -> (KV row, row tile, split)
     const int L = blockIdx.x;
-    const int W = (L & 7) * p.per_xcd + (L >> 3);
-    if (W >= p.total_items) return;
+    const int x = L & 7;
+    int k = L >> 3;
     const Shape& s = p.s;
-    const int split = W % p.splits;
-    const int tmp = W / p.splits;
-    const int tile = tmp % p.ntiles;
-    const int row = tmp / p.ntiles;
-    const int b = row / s.Hkv;
+    int row, b, local;
+    if (p.use_rows) {
+        int i = p.xoff[x];
+        const int iend = p.xoff[x + 1];
+        for (; i < iend; ++i) {
+            const int items = p.ntiles * p.sp[p.xrow[i] / s.Hkv];
+            if (k < items) break;
+            k -= items;
+        }
+        if (i >= iend) return;
+        row = p.xrow[i];
+        b = row / s.Hkv;
+        local = k;
+    } else {
+        const int W = x * p.per_xcd + k;
+        if (W >= p.total_items) return;
+        b = 0;
+        while (b + 1 < s.B && p.ioff[b + 1] <= W) ++b;
+        const int per_row = p.ntiles * p.sp[b];
+        row = b * s.Hkv + (W - p.ioff[b]) / per_row;
+        local = (W - p.ioff[b]) % per_row;
+    }
     const int hk = row - b * s.Hkv;
+    const int nsplit = p.sp[b];
+    const int split = local % nsplit;
+    const int tile = local / nsplit;
     const int G = s.G;
     const int P = p.pb.p[b];
     const int rows_total = p.rows_total;
@@ -123,7 +148,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int lim = P + t_last / 64;
     int n_vis = cnt;
     while (n_vis > 0 && tab[n_vis - 1] > lim) --n_vis;
-    const int chunk = (n_vis + p.splits - 1) / p.splits;
+    const int chunk = (n_vis + nsplit - 1) / nsplit;
     const int e0 = min(n_vis, split * chunk);
     const int e1 = min(n_vis, e0 + chunk);
     // table entries are clamped into [0, nkb) so a corrupt table cannot address outside
@@ -333,7 +358,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     if (qvalid) {
         const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
         const float lse2 = l_run > 0.0f ? m_run + __log2f(l_run) : -__builtin_inff();
-        if (p.splits == 1) {
+        if (nsplit == 1) {
             const int hq = hk * G + qg;
             uint16_t* op = p.out.data + b * p.out.sb + (int64_t)qt * p.out.st + (int64_t)hq * p.out.sh;
 #pragma unroll
@@ -367,7 +392,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     }
 }
 
-// Merge split partials: one packed row per 32 threads, 4 head-dim lanes per thread.
+// Merge split partials: one packed row per 32 threads, 4 head-dim lanes per thread.  Rows of
+// requests with one split were written by the attention kernel and are skipped.
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const Shape& s = p.s;
     const int64_t gid = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
@@ -378,14 +404,16 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const int r = static_cast<int>(gid - (int64_t)row * p.rows_total);
     const int b = row / s.Hkv;
     const int hk = row - b * s.Hkv;
+    const int nsplit = p.sp[b];
+    if (nsplit == 1) return;  // the attention kernel wrote this request's rows directly
     const int t = r / s.G;
     const int g = r - t * s.G;
     float mx = -__builtin_inff();
-    for (int sp = 0; sp < p.splits; ++sp) mx = fmaxf(mx, p.ws_lse[(int64_t)sp * rows_all + gid]);
+    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, p.ws_lse[(int64_t)sp * rows_all + gid]);
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float wsum = 0.0f;
     if (mx != -__builtin_inff()) {
-        for (int sp = 0; sp < p.splits; ++sp) {
+        for (int sp = 0; sp < nsplit; ++sp) {
             const float ls = p.ws_lse[(int64_t)sp * rows_all + gid];
             const float wgt = __builtin_amdgcn_exp2f(ls - mx);
             if (wgt == 0.0f) continue;
@@ -411,23 +439,76 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 
 }  // namespace
 
-int attn_pick_splits(const Shape& s, const PastBlocks& pb) {
+void attn_plan(const Shape& s, const PastBlocks& pb, int forced, SplitPlan* plan) {
     // One workgroup is resident per CU (128 KB of LDS).  A launch wants about two rounds of
-    // them (2 x 256 workgroups) to even out the per-tile work differences, so the block
-    // lists are split when the work items alone do not reach that, keeping at least ~16
-    // blocks per split.
+    // them (2 x 256 workgroups).  Without a forced count, each request's block lists are
+    // split so its work items carry about the same number of blocks as everyone else's
+    // (total work / 512), keeping at least ~16 blocks per split and at most 16 splits.
     const int rows_total = s.Lq * s.G;
     const int ntiles = (rows_total + kBM - 1) / kBM;
-    const int items = s.B * s.Hkv * ntiles;
-    constexpr int kSlots = 2 * 256;  // two resident rounds: smooths the per-tile work imbalance
-    int max_blocks = 0;
-    for (int b = 0; b < s.B; ++b) max_blocks = max(max_blocks, pb.p[b] + s.Qb);
-    int splits = items >= kSlots ? 1 : (kSlots + items / 2) / items;
-    const int by_work = max(1, max_blocks / 16);
-    if (splits > by_work) splits = by_work;
-    if (splits > 16) splits = 16;
-    if (splits < 1) splits = 1;
-    return splits;
+    constexpr int kSlots = 2 * 256;
+    double total = 0.0;
+    for (int b = 0; b < s.B; ++b) total += (double)s.Hkv * ntiles * (pb.p[b] + s.Qb);
+    const double item_blocks = total / kSlots;
+    plan->max = 1;
+    plan->off[0] = 0;
+    for (int b = 0; b < s.B; ++b) {
+        const int nb = pb.p[b] + s.Qb;
+        int sb = forced;
+        if (forced <= 0) {
+            sb = static_cast<int>(nb / item_blocks + 0.5);
+            sb = min(sb, max(1, nb / 16));
+            sb = max(1, min(sb, 16));
+        }
+        plan->s[b] = sb;
+        plan->max = max(plan->max, sb);
+        plan->off[b + 1] = plan->off[b] + s.Hkv * ntiles * sb;
+    }
+    const int rows = s.B * s.Hkv;
+    plan->use_rows = rows <= kPlanRows;
+    if (!plan->use_rows) {
+        plan->per_xcd = (plan->off[s.B] + 7) / 8;
+        return;
+    }
+    // rows longest first (stable), each to the XCD with the least work so far
+    int order[kPlanRows];
+    for (int r = 0; r < rows; ++r) order[r] = r;
+    auto work = [&](int r) { return pb.p[r / s.Hkv] + s.Qb; };
+    for (int i = 1; i < rows; ++i) {
+        const int r = order[i];
+        int j = i;
+        while (j > 0 && work(order[j - 1]) < work(r)) {
+            order[j] = order[j - 1];
+            --j;
+        }
+        order[j] = r;
+    }
+    int64_t load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int items[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int nrow[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint16_t lists[8][kPlanRows];
+    for (int i = 0; i < rows; ++i) {
+        const int r = order[i];
+        int x = 0;
+        for (int c = 1; c < 8; ++c)
+            if (load[c] < load[x] || (load[c] == load[x] && items[c] < items[x])) x = c;
+        lists[x][nrow[x]++] = static_cast<uint16_t>(r);
+        load[x] += (int64_t)work(r) * ntiles;
+        items[x] += ntiles * plan->s[r / s.Hkv];
+    }
+    plan->xoff[0] = 0;
+    plan->per_xcd = 0;
+    for (int x = 0; x < 8; ++x) {
+        for (int i = 0; i < nrow[x]; ++i) plan->xrow[plan->xoff[x] + i] = lists[x][i];
+        plan->xoff[x + 1] = plan->xoff[x] + nrow[x];
+        plan->per_xcd = max(plan->per_xcd, items[x]);
+    }
+}
+
+int attn_pick_splits(const Shape& s, const PastBlocks& pb) {
+    SplitPlan plan;
+    attn_plan(s, pb, 0, &plan);
+    return plan.max;
 }
 
 int64_t attn_workspace_bytes(const Shape& s, int num_splits) {
@@ -449,17 +530,23 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     p.scale_log2 = a.scale * 1.4426950408889634f;
     p.out = a.out;
     p.lse = a.lse;
-    p.splits = a.num_splits;
     p.rows_total = a.s.Lq * a.s.G;
     p.ntiles = (p.rows_total + kBM - 1) / kBM;
-    p.total_items = a.s.B * a.s.Hkv * p.ntiles * p.splits;
-    p.per_xcd = (p.total_items + 7) / 8;
+    SplitPlan plan;
+    attn_plan(a.s, a.pb, a.num_splits, &plan);
+    for (int b = 0; b < CA_MAX_BATCH; ++b) p.sp[b] = b < a.s.B ? plan.s[b] : 1;
+    for (int b = 0; b <= CA_MAX_BATCH; ++b) p.ioff[b] = b <= a.s.B ? plan.off[b] : plan.off[a.s.B];
+    p.total_items = plan.off[a.s.B];
+    p.per_xcd = plan.per_xcd;
+    p.use_rows = plan.use_rows;
+    for (int x = 0; x < 9; ++x) p.xoff[x] = plan.use_rows ? plan.xoff[x] : 0;
+    for (int i = 0; i < kPlanRows; ++i) p.xrow[i] = plan.use_rows && i < plan.xoff[8] ? plan.xrow[i] : 0;
     const int64_t rows_all = (int64_t)a.s.B * a.s.Hkv * p.rows_total;
-    p.ws_o = a.num_splits > 1 ? static_cast<float*>(a.workspace) : nullptr;
-    p.ws_lse = a.num_splits > 1 ? p.ws_o + (int64_t)a.num_splits * rows_all * 128 : nullptr;
+    p.ws_o = plan.max > 1 ? static_cast<float*>(a.workspace) : nullptr;
+    p.ws_lse = plan.max > 1 ? p.ws_o + (int64_t)plan.max * rows_all * 128 : nullptr;
     hipLaunchKernelGGL(attn_fwd_kernel<kNW>, dim3(p.per_xcd * 8), dim3(kNW * 64), 0, stream, p);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || a.num_splits <= 1) return e;
+    if (e != hipSuccess || plan.max <= 1) return e;
     const int64_t blocks = (rows_all + 7) / 8;
     hipLaunchKernelGGL(attn_merge_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, p);
     return hipGetLastError();

@@ -64,10 +64,28 @@ struct AttnArgs {
     float scale;
     SeqAddr out;
     float* lse;
-    int num_splits;
+    int num_splits;  // > 0: every request uses this many splits; 0: per-request plan
     void* workspace;
 };
 
+// Split-KV plan.  Request b's block lists are cut into s[b] pieces (max = the largest,
+// which sizes the workspace).  Work placement: with at most kPlanRows KV rows, whole rows
+// go to XCDs (longest first, each to the least-loaded XCD), so a row's items share one L2
+// and the XCDs carry equal work: xrow[xoff[x] .. xoff[x+1]) lists XCD x's rows in order.
+// Otherwise items are numbered request by request (off[b]) and dealt to XCDs in
+// contiguous ranges.
+constexpr int kPlanRows = 512;
+struct SplitPlan {
+    int32_t s[CA_MAX_BATCH];
+    int32_t off[CA_MAX_BATCH + 1];
+    int max;
+    int use_rows;
+    int per_xcd;  // work items per XCD (grid = 8 * per_xcd)
+    uint16_t xrow[kPlanRows];
+    int32_t xoff[9];
+};
+
+void attn_plan(const Shape& s, const PastBlocks& pb, int forced, SplitPlan* plan);
 int attn_pick_splits(const Shape& s, const PastBlocks& pb);
 int64_t attn_workspace_bytes(const Shape& s, int num_splits);
 hipError_t launch_attn(const AttnArgs& a, hipStream_t stream);

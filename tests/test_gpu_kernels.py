@@ -301,6 +301,13 @@ def test_attention_ragged_batch(gpu):
     _attn_case(gpu, [0, 64 * 5, 64 * 31, 64 * 12], 128, 14, 2, "heads_first", 0, 0.25, seed=41)
 
 
+def test_attention_ragged_split_plan(gpu):
+    """Automatic split-KV plans split each request in proportion to its blocks: here the
+    four requests get 1, 3, 7 and 12 splits, so the merge skips the single-split rows."""
+    _print_case(test="attention_ragged_plan")
+    _attn_case(gpu, [64 * 16, 64 * 60, 64 * 120, 64 * 200], 128, 8, 2, "heads_first", 0, 0.3, seed=43)
+
+
 def test_attention_all_selected_equals_dense(gpu):
     """Keeping every block reduces to dense causal attention (checked against torch fp32 SDPA)."""
     _print_case(test="attention_dense")
