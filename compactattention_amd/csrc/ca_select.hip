@@ -629,18 +629,24 @@ __global__ __launch_bounds__(256) void union_compact_kernel(UnionParams p) {
     uint32_t* hw = lds_words;           // [G][W]
     uint32_t* kvw = lds_words + G * W;  // [W]
     if (p.mode == 0) {
-        for (int i = t; i < G * W; i += 256) hw[i] = 0u;
-        __syncthreads();
-        // every (head, query block, word) of the group's row masks, OR-ed into LDS
+        // thread i owns word w of head g: the OR over the pooled query blocks of the group's
+        // row masks, eight independent loads in flight per batch
         const uint32_t* rm = p.rowmask + (int64_t)(b * s.Hq + hk * G) * s.Qb * W;
-        const int per_g = p.pooled * W;
-        for (int i = t; i < G * per_g; i += 256) {
-            const int g = i / per_g;
-            const int r = i - g * per_g;
-            const int qb = r / W;
-            const int w = r - qb * W;
-            const uint32_t v = rm[((int64_t)g * s.Qb + qb) * W + w];
-            if (v) atomicOr(&hw[g * W + w], v);
+        for (int i = t; i < G * W; i += 256) {
+            const int g = i / W;
+            const int w = i - g * W;
+            const uint32_t* src = rm + (int64_t)g * s.Qb * W + w;
+            uint32_t acc = 0;
+            int qb = 0;
+            for (; qb + 8 <= p.pooled; qb += 8) {
+                uint32_t v[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[k] = src[(int64_t)(qb + k) * W];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc |= v[k];
+            }
+            for (; qb < p.pooled; ++qb) acc |= src[(int64_t)qb * W];
+            hw[i] = acc;
         }
         __syncthreads();
     }
