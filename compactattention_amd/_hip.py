@@ -43,6 +43,8 @@ EXPORTED = (
     "ca_attn_fwd",
     "ca_attn_workspace_size",
     "ca_attn_pick_splits",
+    "ca_attn_decode",
+    "ca_attn_decode_workspace_size",
 )
 
 
@@ -119,6 +121,9 @@ _SIGNATURES = {
                                    _f32, _P(SeqLayout), _vp, _i32, _vp, _i64, _vp]),
     "ca_attn_workspace_size": (ctypes.c_int64, [_P(Dims), _vp, _i32]),
     "ca_attn_pick_splits": (ctypes.c_int32, [_P(Dims), _vp]),
+    "ca_attn_decode": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(KvLayout), _P(KvLayout), _vp, _f32,
+                                      _P(SeqLayout), _vp, _i32, _vp, _i64, _vp]),
+    "ca_attn_decode_workspace_size": (ctypes.c_int64, [_P(Dims), _vp, _i32]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

@@ -78,6 +78,45 @@ int check_dims(const ca_dims* d, const int32_t* past_host, ca::Shape* s, ca::Pas
     return CA_OK;
 }
 
+// Validates dims + per-request KV lengths of a decode call (q_len query rows per request
+// sit at the last q_len positions of its kv_len tokens) and fills the internal shape.
+int check_decode_dims(const ca_dims* d, const int32_t* kv_len, ca::Shape* s, ca::PastBlocks* pb,
+                      int* max_nkb) {
+    if (d == nullptr) return fail(CA_ERR_INVALID, "dims is NULL");
+    if (kv_len == nullptr) return fail(CA_ERR_INVALID, "kv_len_host is NULL");
+    if (d->batch < 1 || d->batch > CA_MAX_BATCH)
+        return fail(d->batch < 1 ? CA_ERR_INVALID : CA_ERR_LIMIT, "batch=%d outside [1, %d]",
+                    d->batch, CA_MAX_BATCH);
+    if (d->q_len < 1 || d->q_len > CA_BLOCK)
+        return fail(CA_ERR_INVALID, "decode q_len=%d outside [1, %d]", d->q_len, CA_BLOCK);
+    if (d->num_q_heads <= 0 || d->num_kv_heads <= 0 || d->num_q_heads % d->num_kv_heads != 0)
+        return fail(CA_ERR_INVALID, "num_q_heads=%d must be a positive multiple of num_kv_heads=%d",
+                    d->num_q_heads, d->num_kv_heads);
+    const int G = d->num_q_heads / d->num_kv_heads;
+    if (G > 16) return fail(CA_ERR_LIMIT, "GQA group size %d > 16", G);
+    if (d->kv_cap < 1 || (int64_t)d->kv_cap * CA_BLOCK > (int64_t)1 << 30)
+        return fail(d->kv_cap < 1 ? CA_ERR_INVALID : CA_ERR_LIMIT, "kv_cap=%d blocks outside [1, 2^24]", d->kv_cap);
+    int mx = 0;
+    for (int b = 0; b < d->batch; ++b) {
+        if (kv_len[b] < d->q_len || (int64_t)kv_len[b] > (int64_t)d->kv_cap * CA_BLOCK)
+            return fail(CA_ERR_INVALID, "kv_len[%d]=%d outside [q_len=%d, 64 * kv_cap=%lld]", b, kv_len[b],
+                        d->q_len, (long long)d->kv_cap * CA_BLOCK);
+        mx = max(mx, (kv_len[b] + CA_BLOCK - 1) / CA_BLOCK);
+        pb->p[b] = 0;
+    }
+    for (int b = d->batch; b < CA_MAX_BATCH; ++b) pb->p[b] = 0;
+    s->B = d->batch;
+    s->Lq = d->q_len;
+    s->Hq = d->num_q_heads;
+    s->Hkv = d->num_kv_heads;
+    s->G = G;
+    s->Qb = 0;
+    s->cap = d->kv_cap;
+    s->words = (d->kv_cap + 31) / 32;
+    *max_nkb = mx;
+    return CA_OK;
+}
+
 int check_seq(const ca_seq_layout* l, const char* name, ca::SeqAddr* out) {
     if (l == nullptr || l->data == nullptr) return fail(CA_ERR_INVALID, "%s is NULL", name);
     if (!aligned16(l->data)) return fail(CA_ERR_INVALID, "%s data must be 16-byte aligned", name);
@@ -281,7 +320,7 @@ int32_t ca_attn_pick_splits(const ca_dims* dims, const int32_t* past_blocks_host
     ca::PastBlocks pb;
     int max_nkb = 0;
     if (check_dims(dims, past_blocks_host, &s, &pb, &max_nkb) != CA_OK) return -1;
-    return ca::attn_pick_splits(s, pb);
+    return ca::attn_pick_splits(s, pb, nullptr);
 }
 
 int64_t ca_attn_workspace_size(const ca_dims* dims, const int32_t* past_blocks_host, int32_t num_splits) {
@@ -289,8 +328,9 @@ int64_t ca_attn_workspace_size(const ca_dims* dims, const int32_t* past_blocks_h
     ca::PastBlocks pb;
     int max_nkb = 0;
     if (check_dims(dims, past_blocks_host, &s, &pb, &max_nkb) != CA_OK) return -1;
-    if (num_splits == 0) num_splits = ca::attn_pick_splits(s, pb);
-    if (num_splits < 1 || num_splits > 16) return fail(CA_ERR_INVALID, "num_splits=%d outside [1, 16]", num_splits);
+    if (num_splits == 0) num_splits = ca::attn_pick_splits(s, pb, nullptr);
+    if (num_splits < 1 || num_splits > ca::kMaxPrefillSplits)
+        return fail(CA_ERR_INVALID, "num_splits=%d outside [0, %d]", num_splits, ca::kMaxPrefillSplits);
     return ca::attn_workspace_bytes(s, num_splits);
 }
 
@@ -310,8 +350,9 @@ int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout*
     if (table_stride < a.s.cap) return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, a.s.cap);
     if (!(scale > 0.0f)) return fail(CA_ERR_INVALID, "scale must be positive");
     if ((int64_t)a.s.Lq * a.s.G > (int64_t)1 << 24) return fail(CA_ERR_LIMIT, "q_len * group too large");
-    if (num_splits < 0 || num_splits > 16) return fail(CA_ERR_INVALID, "num_splits=%d outside [0, 16]", num_splits);
-    const int max_splits = num_splits == 0 ? ca::attn_pick_splits(a.s, a.pb) : num_splits;
+    if (num_splits < 0 || num_splits > ca::kMaxPrefillSplits)
+        return fail(CA_ERR_INVALID, "num_splits=%d outside [0, %d]", num_splits, ca::kMaxPrefillSplits);
+    const int max_splits = num_splits == 0 ? ca::attn_pick_splits(a.s, a.pb, nullptr) : num_splits;
     const int64_t need = ca::attn_workspace_bytes(a.s, max_splits);
     if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
         return fail(CA_ERR_WORKSPACE, "num_splits=%d needs a 16-byte aligned workspace of %lld bytes (got %lld)",
@@ -323,8 +364,52 @@ int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout*
     a.lse = lse;
     a.num_splits = num_splits;
     a.workspace = workspace;
+    a.kv_len = nullptr;
     hipError_t e = ca::launch_attn(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "attn launch");
+    return ok();
+}
+
+int64_t ca_attn_decode_workspace_size(const ca_dims* dims, const int32_t* kv_len_host, int32_t num_splits) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0;
+    if (check_decode_dims(dims, kv_len_host, &s, &pb, &max_nkb) != CA_OK) return -1;
+    if (num_splits == 0) num_splits = ca::attn_pick_splits(s, pb, kv_len_host);
+    if (num_splits < 1 || num_splits > ca::kMaxDecodeSplits)
+        return fail(CA_ERR_INVALID, "num_splits=%d outside [0, %d]", num_splits, ca::kMaxDecodeSplits);
+    return ca::attn_workspace_bytes(s, num_splits);
+}
+
+int ca_attn_decode(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout* k,
+                   const ca_kv_layout* v, const int32_t* kv_len_host, float scale,
+                   const ca_seq_layout* out, float* lse, int32_t num_splits, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+    ca::AttnArgs a;
+    int max_nkb = 0, rc;
+    if ((rc = check_decode_dims(dims, kv_len_host, &a.s, &a.pb, &max_nkb)) != CA_OK) return rc;
+    if ((rc = check_seq(q, "q", &a.q)) != CA_OK) return rc;
+    if ((rc = check_seq(out, "out", &a.out)) != CA_OK) return rc;
+    if ((rc = check_kv(k, "k", max_nkb, &a.k)) != CA_OK) return rc;
+    if ((rc = check_kv(v, "v", max_nkb, &a.v)) != CA_OK) return rc;
+    if (!(scale > 0.0f)) return fail(CA_ERR_INVALID, "scale must be positive");
+    if (num_splits < 0 || num_splits > ca::kMaxDecodeSplits)
+        return fail(CA_ERR_INVALID, "num_splits=%d outside [0, %d]", num_splits, ca::kMaxDecodeSplits);
+    const int max_splits = num_splits == 0 ? ca::attn_pick_splits(a.s, a.pb, kv_len_host) : num_splits;
+    const int64_t need = ca::attn_workspace_bytes(a.s, max_splits);
+    if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+        return fail(CA_ERR_WORKSPACE, "num_splits=%d needs a 16-byte aligned workspace of %lld bytes (got %lld)",
+                    num_splits, (long long)need, (long long)workspace_bytes);
+    a.table = nullptr;
+    a.table_stride = 0;
+    a.counts = nullptr;
+    a.scale = scale;
+    a.lse = lse;
+    a.num_splits = num_splits;
+    a.workspace = workspace;
+    a.kv_len = kv_len_host;
+    hipError_t e = ca::launch_attn(a, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "attn decode launch");
     return ok();
 }
 

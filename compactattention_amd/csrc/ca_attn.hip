@@ -72,6 +72,8 @@ struct AttnParams {
     int per_xcd;      // ceil(total_items / 8)
     float* ws_o;      // [max splits][B*Hkv][rows_total][128]
     float* ws_lse;    // [max splits][B*Hkv][rows_total]  (log2 domain)
+    int32_t qpos0[CA_MAX_BATCH];     // absolute position of each request's query row 0
+    int32_t nkb[CA_MAX_BATCH];       // valid logical blocks of each request
     int32_t sp[CA_MAX_BATCH];        // splits of each request's block lists
     int32_t ioff[CA_MAX_BATCH + 1];  // first work item of each request (linear placement)
     int use_rows;                    // rows placed per XCD (xrow / xoff)
@@ -136,27 +138,31 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int split = local % nsplit;
     const int tile = local / nsplit;
     const int G = s.G;
-    const int P = p.pb.p[b];
+    const int qpos0 = p.qpos0[b];  // query row t sits at absolute position qpos0 + t
+    const int nkb = p.nkb[b];      // valid logical block ids are [0, nkb)
     const int rows_total = p.rows_total;
     const int r0 = tile * BM;
     const int t_first = r0 / G;
     const int t_last = min(r0 + BM - 1, rows_total - 1) / G;
 
-    const int32_t* tab = p.table + (int64_t)row * p.table_stride;
-    const int nkb = P + s.Qb;  // valid logical block ids are [0, nkb)
-    const int cnt = min(max(p.counts[row], 0), s.cap);
-    const int lim = P + t_last / 64;
-    int n_vis = cnt;
-    while (n_vis > 0 && tab[n_vis - 1] > lim) --n_vis;
+    // Without a table (dense decode) the list is the identity 0 .. nkb-1.  Table entries are
+    // clamped into [0, nkb) so a corrupt table cannot address outside the KV tensors.
+    const int32_t* tab = p.table ? p.table + (int64_t)row * p.table_stride : nullptr;
+    auto block_id = [&](int e) { return tab ? min(max(tab[e], 0), nkb - 1) : e; };
+    const int lim = (qpos0 + t_last) >> 6;  // last block the tile can see
+    int n_vis;
+    if (tab) {
+        n_vis = min(max(p.counts[row], 0), s.cap);
+        while (n_vis > 0 && tab[n_vis - 1] > lim) --n_vis;
+    } else {
+        n_vis = min(nkb, lim + 1);
+    }
     const int chunk = (n_vis + nsplit - 1) / nsplit;
     const int e0 = min(n_vis, split * chunk);
     const int e1 = min(n_vis, e0 + chunk);
-    // table entries are clamped into [0, nkb) so a corrupt table cannot address outside
-    // the KV tensors
-    auto block_id = [&](int e) { return min(max(tab[e], 0), nkb - 1); };
     // entries at or after e_mask contain keys beyond the tile's first query position
     int e_mask = e1;
-    while (e_mask > e0 && block_id(e_mask - 1) * 64 + 63 > P * 64 + t_first) --e_mask;
+    while (e_mask > e0 && block_id(e_mask - 1) * 64 + 63 > qpos0 + t_first) --e_mask;
 
     const int tid = threadIdx.x;
     const int w = tid >> 6;
@@ -214,20 +220,27 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int vstok_b = static_cast<int>(p.v.stok) * 2;
     const int k_goff = st_row * kstok_b + (((l & 15) ^ (st_row & 15)) * 16);
     const int v_goff = st_row * vstok_b + (((l & 15) ^ (4 * (st_row & 3))) * 16);
+    // The request holds qpos0 + Lq tokens (kv_len in decode, whole blocks in prefill).  The
+    // buffer range of a block ends after its last existing token, so the rows past kv_len of
+    // a partial block read as zeros, whatever the cache holds there (masked keys get P = 0,
+    // and 0 * V must not meet a non-finite V).  Row offsets go in the VGPR offset, which the
+    // range check covers.
+    const int kv_tokens = qpos0 + s.Lq;
     auto issue_block = [&](int e, int stage) {
         const int kb = block_id(e);
         const int64_t kphys = kpt ? kpt[kb] : kb;
         const int64_t vphys = vpt ? vpt[kb] : kb;
+        const int rows = min(kv_tokens - kb * 64, 64);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(kbase_row + kphys * p.k.sblk), 0, 0x7fffffff, 0x00020000);
+            const_cast<uint16_t*>(kbase_row + kphys * p.k.sblk), 0, rows * kstok_b, 0x00020000);
         const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-            const_cast<uint16_t*>(vbase_row + vphys * p.v.sblk), 0, 0x7fffffff, 0x00020000);
+            const_cast<uint16_t*>(vbase_row + vphys * p.v.sblk), 0, rows * vstok_b, 0x00020000);
         uint8_t* kdst = smem + stage * kStageBytes + wu * 1024;
         uint8_t* vdst = kdst + kKBytes;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, to_lds(kdst + i * 8192), 16, k_goff, i * 32 * kstok_b, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, to_lds(vdst + i * 8192), 16, v_goff, i * 32 * vstok_b, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, to_lds(kdst + i * 8192), 16, k_goff + i * 32 * kstok_b, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, to_lds(vdst + i * 8192), 16, v_goff + i * 32 * vstok_b, 0, 0, 0);
         }
     };
 
@@ -271,8 +284,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         __builtin_amdgcn_s_setprio(0);
         if (masked) {
             // value j of half kt holds key kt*32 + swap23(8*(j/4) + 4*h + j%4)
-            // = kt*32 + 8*h + key_off(j); visible iff kb*64 + key <= 64*P + t
-            const int vis = P * 64 + qtok - kb * 64 - 8 * h;
+            // = kt*32 + 8*h + key_off(j); visible iff kb*64 + key <= qpos0 + t
+            const int vis = qpos0 + qtok - kb * 64 - 8 * h;
 #pragma unroll
             for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
@@ -338,9 +351,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     else if (nblk > 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else wait_dma();
     __syncthreads();
+    // a wave without query rows (short decode tiles) only moves data
+    const bool wave_active = __ballot(qvalid) != 0;
     auto step = [&](int idx, bool masked) {
         if (idx + 3 < nblk) issue_block(e0 + idx + 3, (idx + 3) % kStages);
-        process(block_id(e0 + idx), smem + (idx % kStages) * kStageBytes, masked);
+        if (wave_active) process(block_id(e0 + idx), smem + (idx % kStages) * kStageBytes, masked);
         // block idx+1 must have landed; later blocks may stay in flight
         if (idx + 3 < nblk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         else if (idx + 2 < nblk) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
@@ -439,26 +454,26 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
 
 }  // namespace
 
-void attn_plan(const Shape& s, const PastBlocks& pb, int forced, SplitPlan* plan) {
+void attn_plan(const Shape& s, const int32_t* nkb, int forced, int max_splits, SplitPlan* plan) {
     // One workgroup is resident per CU (128 KB of LDS).  A launch wants about two rounds of
     // them (2 x 256 workgroups).  Without a forced count, each request's block lists are
     // split so its work items carry about the same number of blocks as everyone else's
-    // (total work / 512), keeping at least ~16 blocks per split and at most 16 splits.
+    // (total work / 512), keeping at least ~16 blocks per split and at most max_splits.
     const int rows_total = s.Lq * s.G;
     const int ntiles = (rows_total + kBM - 1) / kBM;
     constexpr int kSlots = 2 * 256;
     double total = 0.0;
-    for (int b = 0; b < s.B; ++b) total += (double)s.Hkv * ntiles * (pb.p[b] + s.Qb);
+    for (int b = 0; b < s.B; ++b) total += (double)s.Hkv * ntiles * nkb[b];
     const double item_blocks = total / kSlots;
     plan->max = 1;
     plan->off[0] = 0;
     for (int b = 0; b < s.B; ++b) {
-        const int nb = pb.p[b] + s.Qb;
+        const int nb = nkb[b];
         int sb = forced;
         if (forced <= 0) {
             sb = static_cast<int>(nb / item_blocks + 0.5);
             sb = min(sb, max(1, nb / 16));
-            sb = max(1, min(sb, 16));
+            sb = max(1, min(sb, max_splits));
         }
         plan->s[b] = sb;
         plan->max = max(plan->max, sb);
@@ -473,7 +488,7 @@ void attn_plan(const Shape& s, const PastBlocks& pb, int forced, SplitPlan* plan
     // rows longest first (stable), each to the XCD with the least work so far
     int order[kPlanRows];
     for (int r = 0; r < rows; ++r) order[r] = r;
-    auto work = [&](int r) { return pb.p[r / s.Hkv] + s.Qb; };
+    auto work = [&](int r) { return nkb[r / s.Hkv]; };
     for (int i = 1; i < rows; ++i) {
         const int r = order[i];
         int j = i;
@@ -505,9 +520,23 @@ void attn_plan(const Shape& s, const PastBlocks& pb, int forced, SplitPlan* plan
     }
 }
 
-int attn_pick_splits(const Shape& s, const PastBlocks& pb) {
+void attn_positions(const Shape& s, const PastBlocks& pb, const int32_t* kv_len, int32_t* qpos0, int32_t* nkb) {
+    for (int b = 0; b < s.B; ++b) {
+        if (kv_len) {  // decode: the q_len query rows are the last positions of kv_len
+            qpos0[b] = kv_len[b] - s.Lq;
+            nkb[b] = (kv_len[b] + 63) / 64;
+        } else {       // chunked prefill: the chunk starts at block P_b
+            qpos0[b] = 64 * pb.p[b];
+            nkb[b] = pb.p[b] + s.Qb;
+        }
+    }
+}
+
+int attn_pick_splits(const Shape& s, const PastBlocks& pb, const int32_t* kv_len) {
+    int32_t qpos0[CA_MAX_BATCH], nkb[CA_MAX_BATCH];
+    attn_positions(s, pb, kv_len, qpos0, nkb);
     SplitPlan plan;
-    attn_plan(s, pb, 0, &plan);
+    attn_plan(s, nkb, 0, kv_len ? kMaxDecodeSplits : kMaxPrefillSplits, &plan);
     return plan.max;
 }
 
@@ -532,8 +561,12 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     p.lse = a.lse;
     p.rows_total = a.s.Lq * a.s.G;
     p.ntiles = (p.rows_total + kBM - 1) / kBM;
+    int32_t nkb[CA_MAX_BATCH];
+    attn_positions(a.s, a.pb, a.kv_len, p.qpos0, nkb);
+    for (int b = 0; b < CA_MAX_BATCH; ++b) p.nkb[b] = b < a.s.B ? nkb[b] : 0;
+    for (int b = a.s.B; b < CA_MAX_BATCH; ++b) p.qpos0[b] = 0;
     SplitPlan plan;
-    attn_plan(a.s, a.pb, a.num_splits, &plan);
+    attn_plan(a.s, nkb, a.num_splits, a.kv_len ? kMaxDecodeSplits : kMaxPrefillSplits, &plan);
     for (int b = 0; b < CA_MAX_BATCH; ++b) p.sp[b] = b < a.s.B ? plan.s[b] : 1;
     for (int b = 0; b <= CA_MAX_BATCH; ++b) p.ioff[b] = b <= a.s.B ? plan.off[b] : plan.off[a.s.B];
     p.total_items = plan.off[a.s.B];

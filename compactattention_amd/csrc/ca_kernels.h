@@ -66,7 +66,11 @@ struct AttnArgs {
     float* lse;
     int num_splits;  // > 0: every request uses this many splits; 0: per-request plan
     void* workspace;
+    const int32_t* kv_len;  // decode: host array of per-request KV lengths (tokens); else null
 };
+
+constexpr int kMaxPrefillSplits = 16;
+constexpr int kMaxDecodeSplits = 64;
 
 // Split-KV plan.  Request b's block lists are cut into s[b] pieces (max = the largest,
 // which sizes the workspace).  Work placement: with at most kPlanRows KV rows, whole rows
@@ -85,8 +89,9 @@ struct SplitPlan {
     int32_t xoff[9];
 };
 
-void attn_plan(const Shape& s, const PastBlocks& pb, int forced, SplitPlan* plan);
-int attn_pick_splits(const Shape& s, const PastBlocks& pb);
+void attn_plan(const Shape& s, const int32_t* nkb, int forced, int max_splits, SplitPlan* plan);
+void attn_positions(const Shape& s, const PastBlocks& pb, const int32_t* kv_len, int32_t* qpos0, int32_t* nkb);
+int attn_pick_splits(const Shape& s, const PastBlocks& pb, const int32_t* kv_len);
 int64_t attn_workspace_bytes(const Shape& s, int num_splits);
 hipError_t launch_attn(const AttnArgs& a, hipStream_t stream);
 

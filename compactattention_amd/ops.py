@@ -99,6 +99,7 @@ class KV:
     tensor: torch.Tensor
     layout: KvLayout
     page_table: Optional[torch.Tensor] = None
+    tokens: Optional[int] = None  # token capacity of a contiguous layout (None when paged)
 
     @staticmethod
     def seq_first(t: torch.Tensor) -> "KV":
@@ -106,7 +107,8 @@ class KV:
         _need_cuda("kv", t, torch.bfloat16)
         if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
             raise ValueError("seq-first KV must be [B, K, Hkv, 128] with a contiguous last dim")
-        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(2), BLOCK * t.stride(1), t.stride(1), None, 0))
+        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(2), BLOCK * t.stride(1), t.stride(1), None, 0),
+                  tokens=t.shape[1])
 
     @staticmethod
     def heads_first(t: torch.Tensor) -> "KV":
@@ -114,7 +116,8 @@ class KV:
         _need_cuda("kv", t, torch.bfloat16)
         if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
             raise ValueError("heads-first KV must be [B, Hkv, K, 128] with a contiguous last dim")
-        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(1), BLOCK * t.stride(2), t.stride(2), None, 0))
+        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(1), BLOCK * t.stride(2), t.stride(2), None, 0),
+                  tokens=t.shape[2])
 
     @staticmethod
     def paged(pool: torch.Tensor, page_table: torch.Tensor) -> "KV":
@@ -304,7 +307,9 @@ def attn_pick_splits(past_blocks: Sequence[int], q_len: int, num_q_heads: int, n
 def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.Tensor, past_blocks: Sequence[int],
              scale: float, kv_cap: int, num_kv_heads: int, out: Optional[torch.Tensor] = None, with_lse: bool = False,
              num_splits: int = 0, workspace: Optional[torch.Tensor] = None):
-    """Indexed attention prefill; q/out [B, Lq, Hq, 128] bf16."""
+    """Indexed attention prefill; q/out [B, Lq, Hq, 128] bf16.  num_splits = 0 splits each
+    request's block list by the library's per-request plan; a positive value splits every
+    row that many ways."""
     B, Lq, Hq, _ = q.shape
     ql = seq_layout(q, "q")
     if out is None:
@@ -316,10 +321,7 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
         raise ValueError("table must be [B*Hkv, >= kv_cap] with contiguous rows")
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     pa = past_array(past_blocks)
-    if num_splits == 0:
-        num_splits = _hip.lib().ca_attn_pick_splits(ctypes.byref(d), pa)
-        if num_splits < 0:
-            raise _hip.CaError(int(num_splits), _hip.last_error())
+    # num_splits = 0 hands the library its per-request split plan
     need = _hip.lib().ca_attn_workspace_size(ctypes.byref(d), pa, int(num_splits))
     if need < 0:
         raise _hip.CaError(int(need), _hip.last_error())
@@ -330,4 +332,47 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
                                  table.data_ptr(), table.stride(0), counts.data_ptr(), pa, float(scale),
                                  ctypes.byref(ol), _ptr(lse), int(num_splits), _ptr(workspace),
                                  int(need), _stream()))
+    return (out, lse) if with_lse else out
+
+
+def attn_decode_workspace_bytes(kv_len: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int,
+                                kv_cap: int, num_splits: int = 0) -> int:
+    d = make_dims(len(kv_len), q_len, num_q_heads, num_kv_heads, kv_cap)
+    n = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), past_array(kv_len), int(num_splits))
+    if n < 0:
+        raise _hip.CaError(int(n), _hip.last_error())
+    return int(n)
+
+
+def attn_decode(q: torch.Tensor, k: KV, v: KV, kv_len: Sequence[int], scale: float, kv_cap: int, num_kv_heads: int,
+                out: Optional[torch.Tensor] = None, with_lse: bool = False, num_splits: int = 0,
+                workspace: Optional[torch.Tensor] = None):
+    """Dense decode attention over the whole cache: q/out [B, q_len, Hq, 128] bf16 (q_len 1..64),
+    the q_len rows being the last positions of each request's kv_len[b] tokens.
+
+    Replaces the q_len == 1 branch of LlamaSeerAttentionChunkedDense.forward
+    (compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:878-894)."""
+    B, Lq, Hq, _ = q.shape
+    if len(kv_len) != B:
+        raise ValueError(f"kv_len has {len(kv_len)} entries for batch {B}")
+    ql = seq_layout(q, "q")
+    if out is None:
+        out = torch.empty_like(q)
+    ol = seq_layout(out, "out")
+    # the kernel moves whole 64-token blocks: contiguous caches must hold the last one entirely
+    need_tok = BLOCK * ((max(int(x) for x in kv_len) + BLOCK - 1) // BLOCK)
+    for name, kv in (("k", k), ("v", v)):
+        if kv.tokens is not None and kv.tokens < need_tok:
+            raise ValueError(f"{name} cache holds {kv.tokens} tokens; decode reads whole blocks up to {need_tok}")
+    d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
+    ka = past_array(kv_len)
+    need = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), ka, int(num_splits))
+    if need < 0:
+        raise _hip.CaError(int(need), _hip.last_error())
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty((need,), dtype=torch.uint8, device=q.device)
+    lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=q.device) if with_lse else None
+    check(_hip.lib().ca_attn_decode(ctypes.byref(d), ctypes.byref(ql), ctypes.byref(k.layout), ctypes.byref(v.layout),
+                                    ka, float(scale), ctypes.byref(ol), _ptr(lse), int(num_splits),
+                                    _ptr(workspace), int(need), _stream()))
     return (out, lse) if with_lse else out

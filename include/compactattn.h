@@ -216,6 +216,27 @@ int64_t ca_attn_workspace_size(const ca_dims* dims, const int32_t* past_blocks_h
 /* The largest per-request split count of ca_attn_fwd's plan for num_splits = 0. */
 int32_t ca_attn_pick_splits(const ca_dims* dims, const int32_t* past_blocks_host);
 
+/*
+ * Dense decode attention over the whole cache (bf16 in, fp32 accumulate, bf16 out).
+ * dims.q_len (1..64) query rows per request are the last q_len positions of its
+ * kv_len_host[b] tokens: row t attends to keys j <= kv_len - q_len + t, read through the
+ * K/V layouts (blocks 0 .. ceil(kv_len/64)-1, page table if given; kv_len need not be a
+ * multiple of 64).  q/out [B, q_len, Hq, 128], lse as ca_attn_fwd.  The block lists are
+ * split KV-wise (num_splits 1..64, or 0 for a per-request plan) and merged by LSE; more
+ * than one split needs ca_attn_decode_workspace_size() bytes of workspace.
+ * Replaces: the q_len == 1 branch of LlamaSeerAttentionChunkedDense.forward
+ * (compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:878-894), i.e.
+ * _dense_prefill_full_kv / flash_attn_with_kvcache over the updated cache.
+ */
+int ca_attn_decode(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout* k,
+                   const ca_kv_layout* v, const int32_t* kv_len_host, float scale,
+                   const ca_seq_layout* out, float* lse, int32_t num_splits, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
+/* Workspace bytes ca_attn_decode needs for num_splits (0 = its per-request plan). */
+int64_t ca_attn_decode_workspace_size(const ca_dims* dims, const int32_t* kv_len_host,
+                                      int32_t num_splits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -213,5 +213,45 @@ def attention(q_bits: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, past_b
     return (out, lse) if with_lse else out
 
 
+def attention_decode(q_bits: np.ndarray, k_bits: np.ndarray, v_bits: np.ndarray, kv_len, scale: float,
+                     with_lse: bool = False):
+    """Dense causal attention of each request's q_len newest tokens over its whole cache.
+
+    The reference routes decode (q_len == 1) to dense attention over the updated cache
+    (compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:878-894 ->
+    compact_attn/modules/dense_prefill.py:117-175, flash_attn_func with causal=True).  With
+    q_len < kv_len that causal mask is aligned bottom-right: query row t sits at position
+    kv_len - q_len + t and sees keys 0 .. kv_len - q_len + t.  Inputs are bf16 bit patterns,
+    the arithmetic is fp64 (numpy); tokens at or past kv_len[b] are never read.
+
+    q [B, Lq, Hq, 128]; k, v [B, Hkv, >= max(kv_len), 128] heads-first.  Returns out
+    [B, Lq, Hq, 128] fp32 (and lse [B, Hq, Lq], natural log, if requested).
+    """
+    B, Lq, Hq, _ = q_bits.shape
+    Hkv = k_bits.shape[1]
+    G = Hq // Hkv
+    q = bf16_bits_to_f32(q_bits).astype(np.float64)
+    out = np.zeros((B, Lq, Hq, D), dtype=np.float32)
+    lse = np.zeros((B, Hq, Lq), dtype=np.float32)
+    t = np.arange(Lq)
+    for b in range(B):
+        n = int(kv_len[b])
+        pos = n - Lq + t  # absolute position of query row t
+        visible = np.arange(n)[None, :] <= pos[:, None]  # [Lq, n]
+        for hk in range(Hkv):
+            k = bf16_bits_to_f32(k_bits[b, hk, :n]).astype(np.float64)
+            v = bf16_bits_to_f32(v_bits[b, hk, :n]).astype(np.float64)
+            for g in range(G):
+                hq = hk * G + g
+                s = (q[b, :, hq] @ k.T) * scale
+                s = np.where(visible, s, -np.inf)
+                m = s.max(axis=1, keepdims=True)
+                p = np.exp(s - m)
+                l = p.sum(axis=1, keepdims=True)
+                out[b, :, hq] = (p @ v) / l
+                lse[b, hq] = (m + np.log(l))[:, 0]
+    return (out, lse) if with_lse else out
+
+
 def num_threads() -> int:
     return int(lib().orc_num_threads())

@@ -95,6 +95,45 @@ def test_layout_and_workspace_validation():
     assert lib.ca_attn_pick_splits(ctypes.byref(d), _past(0)) >= 1
 
 
+@pytest.mark.parametrize("dims,kv_len,code,msg", [
+    (_dims(batch=0), (1,), _hip.CA_ERR_INVALID, "batch"),
+    (_dims(q_len=0), (1,), _hip.CA_ERR_INVALID, "q_len"),
+    (_dims(q_len=65), (100,), _hip.CA_ERR_INVALID, "q_len"),
+    (_dims(q_len=1, num_q_heads=34, num_kv_heads=2), (8,), _hip.CA_ERR_LIMIT, "group size"),
+    (_dims(q_len=4), (3,), _hip.CA_ERR_INVALID, "kv_len[0]"),
+    (_dims(q_len=1, kv_cap=2), (129,), _hip.CA_ERR_INVALID, "kv_len[0]"),
+    (_dims(q_len=1, kv_cap=0), (1,), _hip.CA_ERR_INVALID, "kv_cap"),
+])
+def test_decode_dims_validation(dims, kv_len, code, msg):
+    lib = _hip.lib()
+    rc = lib.ca_attn_decode(ctypes.byref(dims), ctypes.byref(_seq()), ctypes.byref(_kv()), ctypes.byref(_kv()),
+                            _past(*kv_len), 0.1, ctypes.byref(_seq()), None, 1, None, 0, None)
+    assert rc == code
+    assert msg in _hip.last_error()
+
+
+def test_decode_layout_and_workspace_validation():
+    lib = _hip.lib()
+    d = _dims(batch=2, q_len=1, kv_cap=100)
+    kv = _past(70, 6400)
+    call = lambda q, split, ws, wsb, scale=0.1, kvl=kv: lib.ca_attn_decode(  # noqa: E731
+        ctypes.byref(d), ctypes.byref(q), ctypes.byref(_kv()), ctypes.byref(_kv()), kvl, scale,
+        ctypes.byref(_seq()), None, split, ws, wsb, None)
+    assert call(_seq(data=FAKE + 2), 1, None, 0) == _hip.CA_ERR_INVALID
+    assert call(_seq(), 1, None, 0, scale=-1.0) == _hip.CA_ERR_INVALID
+    assert call(_seq(), 65, None, 0) == _hip.CA_ERR_INVALID
+    assert call(_seq(), 4, None, 0) == _hip.CA_ERR_WORKSPACE
+    assert call(_seq(), 0, None, 0) == _hip.CA_ERR_WORKSPACE  # a 100-block row is split by the plan
+    need = lib.ca_attn_decode_workspace_size(ctypes.byref(d), kv, 4)
+    assert need == 4 * 2 * 2 * (1 * 4) * 129 * 4  # splits * B*Hkv * Lq*G rows * 129 floats
+    assert call(_seq(), 4, FAKE, need - 1) == _hip.CA_ERR_WORKSPACE
+    assert lib.ca_attn_decode_workspace_size(ctypes.byref(d), kv, 0) > 0
+    assert lib.ca_attn_decode_workspace_size(ctypes.byref(d), kv, 65) < 0
+    # one request of one block needs no split and no workspace
+    d1 = _dims(batch=1, q_len=1, kv_cap=1)
+    assert lib.ca_attn_decode_workspace_size(ctypes.byref(d1), _past(64), 0) == 0
+
+
 def test_rule_and_select_validation():
     lib = _hip.lib()
     d = _dims()

@@ -324,3 +324,97 @@ def test_attention_all_selected_equals_dense(gpu):
     ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask).permute(0, 2, 1, 3)
     err = (out.float().cpu() - ref).abs()
     assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
+
+
+# ----------------------------------------------------------------------------- decode
+def _decode_case(gpu, kv_len, Lq, Hq, Hkv, layout, splits, seed, with_prefill_check=False):
+    """Dense decode over each request's whole cache against the fp64 oracle.  Cache slots
+    past kv_len hold NaN: the kernel must neither read them into the result nor let them
+    meet zero weights."""
+    B = len(kv_len)
+    cap = (max(kv_len) + 63) // 64
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((B, Lq, Hq, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16)
+    for b, n in enumerate(kv_len):
+        k[b, :, n:] = float("nan")
+        v[b, :, n:] = float("nan")
+    qg = q.to(gpu)
+    if layout == "heads_first":
+        K, V = ops.KV.heads_first(k.to(gpu)), ops.KV.heads_first(v.to(gpu))
+    elif layout == "seq_first":
+        K = ops.KV.seq_first(k.transpose(1, 2).contiguous().to(gpu))
+        V = ops.KV.seq_first(v.transpose(1, 2).contiguous().to(gpu))
+    else:
+        rows = B * Hkv
+        perm = torch.randperm(rows * cap, generator=g).to(torch.int32).view(rows, cap)
+        pool_k = torch.full((rows * cap, 64, 128), float("nan"), dtype=torch.bfloat16)
+        pool_v = torch.full_like(pool_k, float("nan"))
+        pool_k[perm.view(-1).long()] = k.reshape(rows * cap, 64, 128)
+        pool_v[perm.view(-1).long()] = v.reshape(rows * cap, 64, 128)
+        K, V = ops.KV.paged(pool_k.to(gpu), perm.to(gpu)), ops.KV.paged(pool_v.to(gpu), perm.to(gpu))
+    scale = 1.0 / math.sqrt(128)
+    out, lse = ops.attn_decode(qg, K, V, kv_len, scale, cap, Hkv, with_lse=True, num_splits=splits)
+    torch.cuda.synchronize()
+    ref, ref_lse = oracle.attention_decode(bits(q), bits(k), bits(v), kv_len, scale, with_lse=True)
+    got = f32(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    assert err.max() <= ATOL_MAX, err.max()
+    assert err.mean() <= ATOL_MEAN, err.mean()
+    lerr = np.abs(f32(lse) - ref_lse)
+    assert lerr.max() <= 4e-3, lerr.max()
+    return out
+
+
+@pytest.mark.parametrize("splits", [0, 1, 5])
+@pytest.mark.parametrize("layout", ["heads_first", "seq_first", "paged"])
+def test_decode_layouts_and_splits(gpu, layout, splits):
+    _print_case(test="decode", layout=layout, splits=splits)
+    _decode_case(gpu, [1, 777, 64 * 40 + 13], 1, 8, 2, layout, splits, seed=51)
+
+
+@pytest.mark.parametrize("G,Lq", [(1, 1), (4, 3), (7, 5), (8, 64), (16, 1)])
+def test_decode_groups_and_query_rows(gpu, G, Lq):
+    _print_case(test="decode_groups", G=G, Lq=Lq)
+    _decode_case(gpu, [Lq, 64 * 9 + 7, 1000], Lq, 2 * G, 2, "heads_first", 0, seed=60 + G)
+
+
+def test_decode_long_context_plan(gpu):
+    """A 32K-token request beside a short one: the plan splits the long rows (at least 16
+    blocks per split), so the result goes through the LSE merge."""
+    _print_case(test="decode_long")
+    kv = [64 * 512 + 1, 5000]
+    cap = (max(kv) + 63) // 64
+    assert ops.attn_decode_workspace_bytes(kv, 1, 32, 8, cap, 0) >= ops.attn_decode_workspace_bytes(kv, 1, 32, 8, cap,
+                                                                                                     16)
+    _decode_case(gpu, kv, 1, 32, 8, "heads_first", 0, seed=71)
+
+
+def test_decode_equals_prefill_on_aligned_shapes(gpu):
+    """On 64-aligned shapes decode is dense prefill of the last chunk: with one split each,
+    both entry points run the same blocks in the same order and agree bit for bit."""
+    _print_case(test="decode_vs_prefill")
+    past, Lq, Hq, Hkv = [7, 0, 3], 64, 8, 2
+    B, cap = len(past), max(past) + 1
+    g = torch.Generator().manual_seed(81)
+    q = torch.randn((B, Lq, Hq, 128), generator=g).to(torch.bfloat16).to(gpu)
+    k = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16).to(gpu)
+    v = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16).to(gpu)
+    K, V = ops.KV.heads_first(k), ops.KV.heads_first(v)
+    table, counts = ops.dense_table(past, Lq, Hq, Hkv, cap, gpu)
+    scale = 1.0 / math.sqrt(128)
+    pre, pre_lse = ops.attn_fwd(q, K, V, table, counts, past, scale, cap, Hkv, with_lse=True, num_splits=1)
+    dec, dec_lse = ops.attn_decode(q, K, V, [64 * (p + 1) for p in past], scale, cap, Hkv, with_lse=True,
+                                   num_splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(pre.view(torch.int16), dec.view(torch.int16))
+    assert torch.equal(pre_lse, dec_lse)
+
+
+def test_decode_rejects_short_contiguous_cache(gpu):
+    q = torch.zeros((1, 1, 2, 128), dtype=torch.bfloat16, device=gpu)
+    k = torch.zeros((1, 1, 100, 128), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="whole blocks"):
+        ops.attn_decode(q, ops.KV.heads_first(k), ops.KV.heads_first(k), [100], 0.1, 2, 1)

@@ -248,6 +248,58 @@ def test_attention_matches_masked_sdpa_and_dense():
     assert np.abs(out_d - ref.permute(0, 2, 1, 3).numpy()).max() <= 1e-6
 
 
+def test_attention_decode_pins():
+    """Decode (q_len newest tokens over the whole cache, bottom-right causal mask): pinned to
+    torch's lower-right causal SDPA (fp64, ragged and unaligned lengths), to the C oracle's
+    prefill attention on 64-aligned shapes, and to the one-key closed form."""
+    from torch.nn.attention.bias import causal_lower_right
+
+    B, Hq, Hkv, Lq = 3, 6, 2, 5
+    kv_len = [5, 77, 200]
+    q = _bf16((B, Lq, Hq, 128))
+    k = _bf16((B, Hkv, 256, 128))
+    v = _bf16((B, Hkv, 256, 128))
+    nan = oracle.f32_to_bf16_bits(np.array([np.nan], np.float32))[0]
+    for b, n in enumerate(kv_len):  # tokens past kv_len are never read
+        k[b, :, n:] = nan
+        v[b, :, n:] = nan
+    out, lse = oracle.attention_decode(q, k, v, kv_len, 0.09, with_lse=True)
+    assert np.isfinite(out).all() and np.isfinite(lse).all()
+    qf, kf, vf = (oracle.bf16_bits_to_f32(a).astype(np.float64) for a in (q, k, v))
+    for b, n in enumerate(kv_len):
+        qt = torch.tensor(qf[b]).permute(1, 0, 2)[None]  # [1, Hq, Lq, D]
+        kt = torch.tensor(kf[b, :, :n]).repeat_interleave(Hq // Hkv, dim=0)[None]
+        vt = torch.tensor(vf[b, :, :n]).repeat_interleave(Hq // Hkv, dim=0)[None]
+        ref = torch.nn.functional.scaled_dot_product_attention(qt, kt, vt, attn_mask=causal_lower_right(Lq, n),
+                                                               scale=0.09)
+        assert np.abs(out[b] - ref[0].permute(1, 0, 2).numpy()).max() <= 1e-6
+        s = torch.einsum("hqd,hkd->hqk", qt[0], kt[0]) * 0.09
+        s = s.masked_fill(torch.arange(n)[None, :] > (n - Lq + torch.arange(Lq))[:, None], float("-inf"))
+        assert np.abs(lse[b] - torch.logsumexp(s, dim=-1).numpy()).max() <= 1e-5
+
+    # 64-aligned shapes: decode over kv_len = 64 (P + 1) equals prefill of the last block
+    past = [3, 0]
+    Lq = 64
+    cap = 4
+    q = _bf16((2, Lq, Hq, 128))
+    k = _bf16((2, Hkv, cap * 64, 128))
+    v = _bf16((2, Hkv, cap * 64, 128))
+    dense_tab = np.tile(np.arange(cap, dtype=np.int32), (2 * Hkv, 1))
+    counts = np.array([4, 4, 1, 1], np.int32)
+    pre, pre_lse = oracle.attention(q, k, v, past, dense_tab, counts, 0.1, with_lse=True)
+    dec, dec_lse = oracle.attention_decode(q, k, v, [64 * (p + 1) for p in past], 0.1, with_lse=True)
+    assert np.abs(pre - dec).max() <= 1e-6
+    assert np.abs(pre_lse - dec_lse).max() <= 1e-5
+
+    # one key: the output is that key's value row and the log-sum-exp its score
+    q1, k1, v1 = _bf16((1, 1, 2, 128)), _bf16((1, 1, 64, 128)), _bf16((1, 1, 64, 128))
+    o1, l1 = oracle.attention_decode(q1, k1, v1, [1], 0.3, with_lse=True)
+    vv = oracle.bf16_bits_to_f32(v1[0, 0, 0])
+    assert np.array_equal(o1[0, 0, 0], vv) and np.array_equal(o1[0, 0, 1], vv)
+    qq, kk = (oracle.bf16_bits_to_f32(a).astype(np.float64) for a in (q1[0, 0], k1[0, 0, 0]))
+    assert np.abs(l1[0, :, 0] - 0.3 * (qq @ kk)).max() <= 1e-5
+
+
 def test_planted_blocks_recalled_on_config0_shape():
     """Config 0: 256 queries over 8192 KV (P=124, C=4), 32/8 heads, FlashPrefill pooled scores,
     top-k + sink 0 + 2 local blocks at about 25 % post-union keep: the planted blocks are
