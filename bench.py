@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--cpu-tokens", type=int, default=320, help="query tokens in the CPU attention sample")
     ap.add_argument("--no-model", action="store_true", help="skip the config-3 whole-model prefill")
     ap.add_argument("--no-ragged", action="store_true", help="skip the config-4 ragged batch")
+    ap.add_argument("--no-decode", action="store_true", help="skip the dense decode lines")
     ap.add_argument("--model-tokens", type=int, default=131072)
     ap.add_argument("--model-chunk", type=int, default=2048)
     ap.add_argument("--model-layers", type=int, default=32)
@@ -271,6 +272,9 @@ def main() -> int:
     if not args.no_ragged:
         progress("ragged batch")
         result["ragged_batch"] = ragged_batch(dev)
+    if not args.no_decode:
+        progress("decode")
+        result["decode"] = decode_lines(dev)
     if not args.no_model:
         del ch, kc, vc, K, V, kmean, ws, dws
         torch.cuda.empty_cache()
@@ -389,6 +393,49 @@ def ragged_batch(dev, pasts=(16384, 49152, 98304, 131072), chunk=512, hq=28, hkv
         "attn_splits": "per request, max %d" % splits,
         "tok_per_s": round(B * chunk / (path_us * 1e-6), 1),
     }
+
+
+def decode_lines(dev, hq=32, hkv=8):
+    """Dense decode (one new token per request over its whole cache) with Llama-3.1-8B heads:
+    one attention launch (+ split merge) per layer.  HBM-bound: every cached K/V byte is read
+    once, so the figure of merit is cached bytes / launch time against 8 TB/s."""
+    import torch
+
+    from compactattention_amd import ops
+
+    lines = []
+    for kv_len in ([131072], [32768] * 8, [4096, 16384, 65536, 131072]):
+        B = len(kv_len)
+        cap = (max(kv_len) + 63) // 64
+        g = torch.Generator(device=dev).manual_seed(5)
+        k = torch.randn((B, hkv, cap * 64, 128), generator=g, device=dev).to(torch.bfloat16)
+        v = torch.randn((B, hkv, cap * 64, 128), generator=g, device=dev).to(torch.bfloat16)
+        q = torch.randn((B, 1, hq, 128), generator=g, device=dev).to(torch.bfloat16)
+        K, V = ops.KV.heads_first(k), ops.KV.heads_first(v)
+        out = torch.empty_like(q)
+        ws = torch.empty((max(ops.attn_decode_workspace_bytes(kv_len, 1, hq, hkv, cap, 0), 16),),
+                         dtype=torch.uint8, device=dev)
+        fn = lambda: ops.attn_decode(q, K, V, kv_len, 1 / math.sqrt(128), cap, hkv, out=out,  # noqa: E731
+                                     num_splits=0, workspace=ws)
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 50
+        a.record()
+        for _ in range(n):
+            fn()
+        b_.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b_) / n * 1e3
+        kv_bytes = sum(kv_len) * hkv * 128 * 2 * 2
+        lines.append({"kv_len": kv_len, "us_per_layer": round(us, 1),
+                      "hbm_gbps": round(kv_bytes / (us * 1e-6) / 1e9, 1),
+                      "hbm_frac": round(kv_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)})
+        del k, v, q, K, V, out, ws
+        torch.cuda.empty_cache()
+    return {"workload": f"dense decode, 1 query token per request, {hq} Q / {hkv} KV heads, d 128, bf16 cache; "
+                        "per-request split plan + LSE merge", "lines": lines}
 
 
 def measured_traffic():

@@ -101,7 +101,9 @@ __device__ __forceinline__ void wait_dma() {
 // workgroup owns BM = 32*NW rows.  Registers stay within 256 per lane, which lets two waves
 // share a SIMD: one wave's softmax overlaps the other's MFMAs.  One 8-wave workgroup per
 // CU (128 KB of LDS).
-template <int NW>
+// kTab: block lists come from the per-row table (prefill); otherwise they are the identity
+// 0 .. nkb-1 (dense decode).
+template <int NW, bool kTab>
 __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) void attn_fwd_kernel(AttnParams p) {
     constexpr int BM = 32 * NW;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kStages * kStageBytes];  // [stage]: K rows, then V rows
@@ -145,13 +147,13 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int t_first = r0 / G;
     const int t_last = min(r0 + BM - 1, rows_total - 1) / G;
 
-    // Without a table (dense decode) the list is the identity 0 .. nkb-1.  Table entries are
-    // clamped into [0, nkb) so a corrupt table cannot address outside the KV tensors.
-    const int32_t* tab = p.table ? p.table + (int64_t)row * p.table_stride : nullptr;
-    auto block_id = [&](int e) { return tab ? min(max(tab[e], 0), nkb - 1) : e; };
+    // Table entries are clamped into [0, nkb) so a corrupt table cannot address outside the
+    // KV tensors.
+    const int32_t* tab = kTab ? p.table + (int64_t)row * p.table_stride : nullptr;
+    auto block_id = [&](int e) { return kTab ? min(max(tab[e], 0), nkb - 1) : e; };
     const int lim = (qpos0 + t_last) >> 6;  // last block the tile can see
     int n_vis;
-    if (tab) {
+    if (kTab) {
         n_vis = min(max(p.counts[row], 0), s.cap);
         while (n_vis > 0 && tab[n_vis - 1] > lim) --n_vis;
     } else {
@@ -351,11 +353,9 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     else if (nblk > 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     else wait_dma();
     __syncthreads();
-    // a wave without query rows (short decode tiles) only moves data
-    const bool wave_active = __ballot(qvalid) != 0;
     auto step = [&](int idx, bool masked) {
         if (idx + 3 < nblk) issue_block(e0 + idx + 3, (idx + 3) % kStages);
-        if (wave_active) process(block_id(e0 + idx), smem + (idx % kStages) * kStageBytes, masked);
+        process(block_id(e0 + idx), smem + (idx % kStages) * kStageBytes, masked);
         // block idx+1 must have landed; later blocks may stay in flight
         if (idx + 3 < nblk) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
         else if (idx + 2 < nblk) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
@@ -408,7 +408,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 }
 
 // Merge split partials: one packed row per 32 threads, 4 head-dim lanes per thread.  Rows of
-// requests with one split were written by the attention kernel and are skipped.
+// requests with one split were written by the attention kernel and are skipped.  The
+// 32 threads of a row first spread its (at most 64) split log-sum-exps over their lanes, so
+// the max and the weights take two loads per thread, then add the partial outputs eight
+// splits at a time with the loads issued together.
+static_assert(kMaxPrefillSplits <= 64 && kMaxDecodeSplits <= 64, "the merge holds two splits per lane");
 __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const Shape& s = p.s;
     const int64_t gid = (int64_t)blockIdx.x * 8 + (threadIdx.x >> 5);
@@ -423,48 +427,355 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     if (nsplit == 1) return;  // the attention kernel wrote this request's rows directly
     const int t = r / s.G;
     const int g = r - t * s.G;
-    float mx = -__builtin_inff();
-    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, p.ws_lse[(int64_t)sp * rows_all + gid]);
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    float wsum = 0.0f;
-    if (mx != -__builtin_inff()) {
-        for (int sp = 0; sp < nsplit; ++sp) {
-            const float ls = p.ws_lse[(int64_t)sp * rows_all + gid];
-            const float wgt = __builtin_amdgcn_exp2f(ls - mx);
-            if (wgt == 0.0f) continue;
-            const float4 o = *reinterpret_cast<const float4*>(p.ws_o + ((int64_t)sp * rows_all + gid) * 128 + 4 * lane);
-            acc[0] += wgt * o.x;
-            acc[1] += wgt * o.y;
-            acc[2] += wgt * o.z;
-            acc[3] += wgt * o.w;
-            wsum += wgt;
+    // lane holds splits lane and lane + 32
+    const float ls0 = lane < nsplit ? p.ws_lse[(int64_t)lane * rows_all + gid] : -__builtin_inff();
+    const float ls1 = lane + 32 < nsplit ? p.ws_lse[(int64_t)(lane + 32) * rows_all + gid] : -__builtin_inff();
+    float mx = fmaxf(ls0, ls1);
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 32));
+    const bool any = mx != -__builtin_inff();
+    const float w0 = any ? __builtin_amdgcn_exp2f(ls0 - mx) : 0.0f;  // 0 for absent or empty splits
+    const float w1 = any ? __builtin_amdgcn_exp2f(ls1 - mx) : 0.0f;
+    float wsum = w0 + w1;
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) wsum += __shfl_xor(wsum, o, 32);
+    float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const float* wo = p.ws_o + gid * 128 + 4 * lane;
+    for (int sp0 = 0; sp0 < nsplit; sp0 += 8) {
+        float4 o[8];
+        float wgt[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int sp = sp0 + u;
+            const float wa = __shfl(w0, sp & 31, 32);
+            const float wb = __shfl(w1, sp & 31, 32);
+            wgt[u] = sp < nsplit ? (sp < 32 ? wa : wb) : 0.0f;
+            o[u] = wgt[u] != 0.0f ? *reinterpret_cast<const float4*>(wo + (int64_t)sp * rows_all * 128)
+                                  : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            acc.x += wgt[u] * o[u].x;
+            acc.y += wgt[u] * o[u].y;
+            acc.z += wgt[u] * o[u].z;
+            acc.w += wgt[u] * o[u].w;
         }
     }
     const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
     const int hq = hk * s.G + g;
     uint16_t* op = p.out.data + b * p.out.sb + (int64_t)t * p.out.st + (int64_t)hq * p.out.sh + 4 * lane;
-    f32x4_t o4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) o4[i] = acc[i] * inv;
+    f32x4_t o4 = {acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv};
     *reinterpret_cast<bf16x4_t*>(op) = __builtin_convertvector(o4, bf16x4_t);
     if (p.lse && lane == 0)
         p.lse[((int64_t)b * s.Hq + hq) * s.Lq + t] =
             wsum > 0.0f ? (mx + __log2f(wsum)) * 0.69314718055994531f : -__builtin_inff();
 }
 
+// ---------------------------------------------------------------------------------------
+// Dense decode with at most 16 packed query rows per KV row (q_len * G <= 16), e.g. one new
+// token per request.  The work is HBM-bound (every cached byte is read once) and too narrow
+// for 32-row tiles, so the shape differs from attn_fwd_kernel:
+//  - 16x16x32 MFMAs (v_mfma_f32_16x16x32_bf16): S^T = K Q^T over 16-key tiles and
+//    O^T += V^T P^T over 16-wide head-dim tiles, with the 16 packed rows as the N dimension;
+//  - each of the 8 waves runs its own stream of blocks (e0 + w, e0 + w + 8, ...) with its
+//    own online softmax, so eight blocks are in flight per CU and the waves' MFMA, softmax
+//    and memory phases overlap; the eight partial results merge through LDS at the end;
+//  - K goes straight from HBM into the MFMA A-operand registers (each lane loads 16 bytes
+//    of one key row per 32-d step); V goes through the wave's own 16 KB of LDS (LDS DMA,
+//    16-byte chunk c of row r at c ^ 2 (r & 7)) to be read transposed by ds_read_b64_tr_b16.
+// The A-row -> key map of the P^T operand is permuted so that P comes straight out of the
+// S^T accumulators: k-index (g, i) of 32-key step ks is key 32 ks + 16 (i / 4) + 4 g + i % 4
+// for lane group g = lane / 16, and the transposed V reads follow the same map.
+constexpr int kDecWaves = 8;
+constexpr int kDecRows = 16;
+constexpr int kDecVBytes = 64 * 256;
+constexpr int kDecOStride = 132;  // floats per row of a wave's partial O in LDS (padded)
+
+__global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams p) {
+    __shared__ __attribute__((aligned(16))) uint8_t smem[kDecWaves * kDecVBytes];
+
+    const int L = blockIdx.x;
+    const int x = L & 7;
+    int k = L >> 3;
+    const Shape& s = p.s;
+    int row, b, local;
+    if (p.use_rows) {
+        int i = p.xoff[x];
+        const int iend = p.xoff[x + 1];
+        for (; i < iend; ++i) {
+            const int items = p.sp[p.xrow[i] / s.Hkv];
+            if (k < items) break;
+            k -= items;
+        }
+        if (i >= iend) return;
+        row = p.xrow[i];
+        b = row / s.Hkv;
+        local = k;
+    } else {
+        const int W = x * p.per_xcd + k;
+        if (W >= p.total_items) return;
+        b = 0;
+        while (b + 1 < s.B && p.ioff[b + 1] <= W) ++b;
+        const int per_row = p.sp[b];
+        row = b * s.Hkv + (W - p.ioff[b]) / per_row;
+        local = (W - p.ioff[b]) % per_row;
+    }
+    const int hk = row - b * s.Hkv;
+    const int nsplit = p.sp[b];
+    const int split = local;
+    const int G = s.G;
+    const int R = p.rows_total;
+    const int qpos0 = p.qpos0[b];
+    const int nkb = p.nkb[b];  // the last query row sees every block
+    const int chunk = (nkb + nsplit - 1) / nsplit;
+    const int e0 = min(nkb, split * chunk);
+    const int e1 = min(nkb, e0 + chunk);
+    const int e_mask = (qpos0 + 1) >> 6;  // blocks from here on hold keys past query row 0
+
+    const int tid = threadIdx.x;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l = tid & 63;
+    const int n = l & 15;  // packed query row (N index)
+    const int g = l >> 4;  // lane group (K index block)
+
+    // Q^T (B operand of S^T): lane (n, g) holds Q[row n][32 j + 8 g .. + 7] for step j
+    const bool qvalid = n < R;
+    const int qt = qvalid ? n / G : 0;
+    const int qg = qvalid ? n - qt * G : 0;
+    bf16x8_t qf[4];
+    {
+        const uint16_t* qp = p.q.data + b * p.q.sb + (int64_t)qt * p.q.st + (int64_t)(hk * G + qg) * p.q.sh + 8 * g;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (qvalid) {
+                qf[j] = *reinterpret_cast<const bf16x8_t*>(qp + 32 * j);
+            } else {
+                u32x4_t z = {0u, 0u, 0u, 0u};
+                qf[j] = __builtin_bit_cast(bf16x8_t, z);
+            }
+        }
+    }
+    const int qpos = qpos0 + qt;  // absolute position of this lane's query row
+
+    const uint16_t* kbase_row = p.k.data + b * p.k.sb + hk * p.k.sh;
+    const uint16_t* vbase_row = p.v.data + b * p.v.sb + hk * p.v.sh;
+    const int32_t* kpt = p.k.page_table ? p.k.page_table + (int64_t)row * p.k.pts : nullptr;
+    const int32_t* vpt = p.v.page_table ? p.v.page_table + (int64_t)row * p.v.pts : nullptr;
+    const int kstok_b = static_cast<int>(p.k.stok) * 2;
+    const int vstok_b = static_cast<int>(p.v.stok) * 2;
+    const int kv_tokens = qpos0 + s.Lq;
+    uint8_t* vbuf = smem + w * kDecVBytes;
+
+    // A step is half a block (32 keys).  K (A operand of S^T) for key tile kt and 32-d step
+    // j: lane (n, g) loads the 16 bytes at d = 32 j + 8 g of the half's key row 16 kt + n.
+    // Buffer ranges end after the block's last existing token (rows past kv_len read as
+    // zeros).
+    int k_off[2];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) k_off[kt] = (16 * kt + n) * kstok_b + 16 * g;
+    // V DMA: instruction i writes the half's LDS rows 4 i .. 4 i + 3; lane L fills row
+    // 4 i + L / 16 at chunk position L & 15, which holds global chunk (L & 15) ^ 2 (row & 7).
+    int v_goff[2];
+#pragma unroll
+    for (int par = 0; par < 2; ++par)
+        v_goff[par] = (l >> 4) * vstok_b + (((l & 15) ^ (2 * (4 * par + (l >> 4)))) * 16);
+    // V^T fragment (A operand of O^T) for d-tile dt: lane (a = l & 15, g) reads 8 bytes at
+    // half row 16 hh + 4 g + a / 4, d = 16 dt + 4 (a & 3).
+    int v_off[8];
+    {
+        const int a = l & 15;
+        const int rr = 4 * g + (a >> 2);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) v_off[dt] = rr * 256 + 32 * (dt ^ (rr & 7)) + 8 * (a & 3);
+    }
+
+    // Two register sets for K and two 8 KB LDS halves for V: the loads of step st + 1 are in
+    // flight while step st is computed.  One step is 8 K loads + 8 V DMA loads per wave.
+    u32x4_t kf[2][2][4];
+    uint8_t* vhalf[2] = {vbuf, vbuf + kDecVBytes / 2};
+    auto block_rsrc = [&](const uint16_t* base, const int32_t* pt, int64_t sblk, int kb, int stok_b) {
+        const int64_t phys = pt ? pt[kb] : kb;
+        const int rows = min(kv_tokens - kb * 64, 64);
+        return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + phys * sblk), 0, rows * stok_b,
+                                                 0x00020000);
+    };
+    const int nb_w = e0 + w < e1 ? (e1 - 1 - (e0 + w)) / kDecWaves + 1 : 0;  // this wave's blocks
+    const int nsteps = 2 * nb_w;
+    auto step_block = [&](int st) { return e0 + w + kDecWaves * (st >> 1); };
+    auto issue = [&](int st, int set) {
+        const int kb = step_block(st);
+        const int half = st & 1;
+        const __amdgpu_buffer_rsrc_t rk = block_rsrc(kbase_row, kpt, p.k.sblk, kb, kstok_b);
+        const __amdgpu_buffer_rsrc_t rv = block_rsrc(vbase_row, vpt, p.v.sblk, kb, vstok_b);
+        const int kh = 32 * half * kstok_b;
+        const int vh = 32 * half * vstok_b;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                kf[set][kt][j] = __builtin_amdgcn_raw_buffer_load_b128(rk, kh + k_off[kt] + 64 * j, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, to_lds(vhalf[set] + i * 1024), 16,
+                                                     vh + v_goff[i & 1] + 4 * i * vstok_b, 0, 0, 0);
+    };
+
+    const float sl2 = p.scale_log2;
+    f32x4_t oacc[8];
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_run = -__builtin_inff();
+    float l_run = 0.0f;
+    const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+
+    auto compute = [&](int st, int set) {
+        const int kb = step_block(st);
+        const int half = st & 1;
+        f32x4_t sacc[2];
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) sacc[kt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+                sacc[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, kf[set][kt][j]), qf[j],
+                                                                  sacc[kt], 0, 0, 0);
+        if (kb >= e_mask) {
+            // value i of tile kt is key 64 kb + 32 half + 16 kt + 4 g + i
+            const int vis = qpos - kb * 64 - 32 * half - 4 * g;
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (16 * kt + i > vis) sacc[kt][i] = -__builtin_inff();
+        }
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kt][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+        float alpha = 1.0f;
+        if (mx > m_run + kRescale) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mx);
+            m_run = mx;
+            l_run *= alpha;
+        }
+        if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < 8; ++dt) oacc[dt] *= alpha;
+        }
+        const float m_use = m_run == -__builtin_inff() ? 0.0f : m_run;
+        f32x8_t pv8;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pv8[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[i >> 2][i & 3], sl2, -m_use));
+        const bf16x8_t pf = __builtin_convertvector(pv8, bf16x8_t);
+        // the normaliser sums the bf16-rounded weights the PV product uses
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 0, 1), ones, l_run, false);
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 2, 3), ones, l_run, false);
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 4, 5), ones, l_run, false);
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf, pf, 6, 7), ones, l_run, false);
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+            const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(to_lds_v4(vhalf[set] + v_off[dt]));
+            const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(to_lds_v4(vhalf[set] + v_off[dt] + 4096));
+            const bf16x8_t a = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, pf, oacc[dt], 0, 0, 0);
+        }
+    };
+
+    // nsteps is even: both halves of every block
+    if (nsteps > 0) issue(0, 0);
+    for (int st = 0; st < nsteps; st += 2) {
+        issue(st + 1, 1);
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");  // step st has landed
+        compute(st, 0);
+        if (st + 2 < nsteps) {
+            // the transposed reads of step st have returned before the DMA reuses its half
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            issue(st + 2, 0);
+            asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+        } else {
+            wait_dma();
+        }
+        compute(st + 1, 1);
+    }
+
+    // ---- merge the eight waves' partial results through LDS ----
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    __syncthreads();  // every wave is done with its V rows
+    float* mo = reinterpret_cast<float*>(smem);
+    float* ml = mo + kDecWaves * kDecRows * kDecOStride;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<f32x4_t*>(mo + (w * kDecRows + n) * kDecOStride + 16 * dt + 4 * g) = oacc[dt];
+    if (g == 0) {
+        ml[(w * kDecRows + n) * 2 + 0] = m_run;
+        ml[(w * kDecRows + n) * 2 + 1] = l_run;
+    }
+    __syncthreads();
+    const int orow = tid >> 5;  // 16 rows x 32 threads, 4 head-dim values each
+    const int d4 = (tid & 31) * 4;
+    if (orow >= R) return;
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int v = 0; v < kDecWaves; ++v) mx = fmaxf(mx, ml[(v * kDecRows + orow) * 2]);
+    f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    float wsum = 0.0f;
+    if (mx != -__builtin_inff()) {
+#pragma unroll
+        for (int v = 0; v < kDecWaves; ++v) {
+            const float wv = __builtin_amdgcn_exp2f(ml[(v * kDecRows + orow) * 2] - mx);
+            wsum += wv * ml[(v * kDecRows + orow) * 2 + 1];
+            acc += wv * *reinterpret_cast<const f32x4_t*>(mo + (v * kDecRows + orow) * kDecOStride + d4);
+        }
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+    const float lse2 = wsum > 0.0f ? mx + __log2f(wsum) : -__builtin_inff();
+    acc *= inv;
+    const int ot = orow / G;
+    const int og = orow - ot * G;
+    if (nsplit == 1) {
+        const int hq = hk * G + og;
+        uint16_t* op = p.out.data + b * p.out.sb + (int64_t)ot * p.out.st + (int64_t)hq * p.out.sh + d4;
+        *reinterpret_cast<bf16x4_t*>(op) = __builtin_convertvector(acc, bf16x4_t);
+        if (p.lse && (tid & 31) == 0) p.lse[((int64_t)b * s.Hq + hq) * s.Lq + ot] = lse2 * 0.69314718055994531f;
+    } else {
+        const int64_t prow = ((int64_t)split * (s.B * s.Hkv) + row) * R + orow;
+        *reinterpret_cast<f32x4_t*>(p.ws_o + prow * 128 + d4) = acc;
+        if ((tid & 31) == 0) p.ws_lse[prow] = lse2;
+    }
+}
+
 }  // namespace
 
-void attn_plan(const Shape& s, const int32_t* nkb, int forced, int max_splits, SplitPlan* plan) {
-    // One workgroup is resident per CU (128 KB of LDS).  A launch wants about two rounds of
-    // them (2 x 256 workgroups).  Without a forced count, each request's block lists are
-    // split so its work items carry about the same number of blocks as everyone else's
-    // (total work / 512), keeping at least ~16 blocks per split and at most max_splits.
+bool attn_uses_decode_kernel(const Shape& s, bool dense) {
+    return dense && s.Lq * s.G <= kDecRows;
+}
+
+void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, SplitPlan* plan) {
+    // One workgroup is resident per CU (128 KB of LDS).  Without a forced count, each
+    // request's block lists are split so its work items carry about the same number of
+    // blocks as everyone else's (total work / slots), keeping a minimum number of blocks
+    // per split and at most the entry point's maximum of splits.
+    //  - indexed prefill (attn_fwd_kernel): about two rounds of workgroups (2 x 256 slots),
+    //    at least ~16 blocks per split, at most 16 splits;
+    //  - dense decode with <= 16 rows (attn_decode_kernel): one round (256 slots), at least
+    //    ~32 blocks per split (4 per wave), at most 64 splits.  Its eight waves stream
+    //    blocks on their own, so one long item per CU beats two shorter ones.
+    //  - dense decode with more rows runs attn_fwd_kernel with the prefill sizing and up to
+    //    64 splits.
+    const bool dec = attn_uses_decode_kernel(s, dense);
+    const int slots = dec ? 256 : 512;
+    const int min_blocks = dec ? 32 : 16;
+    const int max_splits = dense ? kMaxDecodeSplits : kMaxPrefillSplits;
     const int rows_total = s.Lq * s.G;
-    const int ntiles = (rows_total + kBM - 1) / kBM;
-    constexpr int kSlots = 2 * 256;
+    const int ntiles = dec ? 1 : (rows_total + kBM - 1) / kBM;
     double total = 0.0;
     for (int b = 0; b < s.B; ++b) total += (double)s.Hkv * ntiles * nkb[b];
-    const double item_blocks = total / kSlots;
+    const double item_blocks = total / slots;
     plan->max = 1;
     plan->off[0] = 0;
     for (int b = 0; b < s.B; ++b) {
@@ -472,7 +783,7 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, int max_splits, S
         int sb = forced;
         if (forced <= 0) {
             sb = static_cast<int>(nb / item_blocks + 0.5);
-            sb = min(sb, max(1, nb / 16));
+            sb = min(sb, max(1, nb / min_blocks));
             sb = max(1, min(sb, max_splits));
         }
         plan->s[b] = sb;
@@ -536,7 +847,7 @@ int attn_pick_splits(const Shape& s, const PastBlocks& pb, const int32_t* kv_len
     int32_t qpos0[CA_MAX_BATCH], nkb[CA_MAX_BATCH];
     attn_positions(s, pb, kv_len, qpos0, nkb);
     SplitPlan plan;
-    attn_plan(s, nkb, 0, kv_len ? kMaxDecodeSplits : kMaxPrefillSplits, &plan);
+    attn_plan(s, nkb, 0, kv_len != nullptr, &plan);
     return plan.max;
 }
 
@@ -566,7 +877,7 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     for (int b = 0; b < CA_MAX_BATCH; ++b) p.nkb[b] = b < a.s.B ? nkb[b] : 0;
     for (int b = a.s.B; b < CA_MAX_BATCH; ++b) p.qpos0[b] = 0;
     SplitPlan plan;
-    attn_plan(a.s, nkb, a.num_splits, a.kv_len ? kMaxDecodeSplits : kMaxPrefillSplits, &plan);
+    attn_plan(a.s, nkb, a.num_splits, a.kv_len != nullptr, &plan);
     for (int b = 0; b < CA_MAX_BATCH; ++b) p.sp[b] = b < a.s.B ? plan.s[b] : 1;
     for (int b = 0; b <= CA_MAX_BATCH; ++b) p.ioff[b] = b <= a.s.B ? plan.off[b] : plan.off[a.s.B];
     p.total_items = plan.off[a.s.B];
@@ -577,7 +888,12 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     const int64_t rows_all = (int64_t)a.s.B * a.s.Hkv * p.rows_total;
     p.ws_o = plan.max > 1 ? static_cast<float*>(a.workspace) : nullptr;
     p.ws_lse = plan.max > 1 ? p.ws_o + (int64_t)plan.max * rows_all * 128 : nullptr;
-    hipLaunchKernelGGL(attn_fwd_kernel<kNW>, dim3(p.per_xcd * 8), dim3(kNW * 64), 0, stream, p);
+    if (a.table)
+        hipLaunchKernelGGL((attn_fwd_kernel<kNW, true>), dim3(p.per_xcd * 8), dim3(kNW * 64), 0, stream, p);
+    else if (attn_uses_decode_kernel(a.s, true))
+        hipLaunchKernelGGL(attn_decode_kernel, dim3(p.per_xcd * 8), dim3(kDecWaves * 64), 0, stream, p);
+    else
+        hipLaunchKernelGGL((attn_fwd_kernel<kNW, false>), dim3(p.per_xcd * 8), dim3(kNW * 64), 0, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || plan.max <= 1) return e;
     const int64_t blocks = (rows_all + 7) / 8;

@@ -89,7 +89,9 @@ struct SplitPlan {
     int32_t xoff[9];
 };
 
-void attn_plan(const Shape& s, const int32_t* nkb, int forced, int max_splits, SplitPlan* plan);
+// dense = identity block lists over kv_len tokens (decode); otherwise per-row tables
+void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, SplitPlan* plan);
+bool attn_uses_decode_kernel(const Shape& s, bool dense);
 void attn_positions(const Shape& s, const PastBlocks& pb, const int32_t* kv_len, int32_t* qpos0, int32_t* nkb);
 int attn_pick_splits(const Shape& s, const PastBlocks& pb, const int32_t* kv_len);
 int64_t attn_workspace_bytes(const Shape& s, int num_splits);
