@@ -59,6 +59,8 @@ class PagedKVCache:
             raise ValueError("k_new does not match the cache's batch / KV heads")
         if L % BLOCK:
             raise ValueError("appended chunks must be multiples of 64 tokens")
+        if self.length % BLOCK:
+            raise ValueError("chunked prefill cannot follow decode steps that left a partial block")
         if self.length + L > self.cap * BLOCK:
             raise ValueError(f"cache capacity {self.cap * BLOCK} tokens exceeded")
         if gate_wk is not None and self.kgate is None:
@@ -69,6 +71,22 @@ class PagedKVCache:
                        rope_sin=rope_sin, kgate=self.kgate if gate_wk is not None else None)
         self.length += L
         return past
+
+    def append_tokens(self, k_new: torch.Tensor, v_new: torch.Tensor) -> int:
+        """Decode append: [B, L, Hkv, 128] bf16 K/V (any L) at the current length, which need
+        not be block-aligned; returns the length before the append.  Block summaries are
+        not maintained for these tokens, so chunked prefill cannot follow decode steps
+        (append() rejects a length that is not a multiple of 64)."""
+        B, L, Hkv, _ = k_new.shape
+        if B != self.batch or Hkv != self.num_kv_heads:
+            raise ValueError("k_new does not match the cache's batch / KV heads")
+        if self.length + L > self.cap * BLOCK:
+            raise ValueError(f"cache capacity {self.cap * BLOCK} tokens exceeded")
+        start = self.length
+        self.k[:, :, start:start + L].copy_(k_new.transpose(1, 2))
+        self.v[:, :, start:start + L].copy_(v_new.transpose(1, 2))
+        self.length += L
+        return start
 
     def k_hf(self) -> torch.Tensor:
         return self.k[:, :, :self.length]

@@ -20,6 +20,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from ... import ops
 from ...kv_cache import PagedKVCache
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 
@@ -90,6 +91,31 @@ def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, si
     return (qf * c + rotate_half(qf) * s).to(q.dtype), (kf * c + rotate_half(kf) * s).to(k.dtype)
 
 
+def dense_decode_forward(attn: nn.Module, hidden_states: torch.Tensor, position_embeddings, cache: PagedKVCache):
+    """Decode step(s) of a compactattn attention module: up to 64 new tokens per request
+    attend densely to the whole cache (the reference routes q_len == 1 to dense attention,
+    compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:878-894).
+    K/V of the new tokens are appended at the cache's current length."""
+    B, L, _ = hidden_states.shape
+    if L > BLOCK:
+        raise ValueError(f"decode steps take at most {BLOCK} tokens per call (got {L})")
+    q = attn.q_proj(hidden_states).view(B, L, attn.num_heads, attn.head_dim)
+    k = attn.k_proj(hidden_states).view(B, L, attn.num_key_value_heads, attn.head_dim)
+    v = attn.v_proj(hidden_states).view(B, L, attn.num_key_value_heads, attn.head_dim)
+    cos, sin = position_embeddings
+    query_states, key_states = apply_rotary_pos_emb(q, k, cos, sin)
+    cache.append_tokens(key_states, v)
+    K, V = cache.layouts()
+    out = ops.attn_decode(query_states.contiguous(), K, V, [cache.length] * B, attn.scaling, cache.cap,
+                          attn.num_key_value_heads)
+    return attn.o_proj(out.reshape(B, L, -1))
+
+
+def is_decode_step(hidden_states: torch.Tensor, cache: PagedKVCache) -> bool:
+    """Fewer than 64 new tokens, or a cache already past a block boundary, is decode."""
+    return hidden_states.shape[1] < BLOCK or cache.length % BLOCK != 0
+
+
 class ChunkedPrefillCache:
     """One PagedKVCache per layer (all layers advance together)."""
 
@@ -155,7 +181,8 @@ class CompactAttnLlamaModel(nn.Module):
 
 class CompactAttnLlamaForCausalLM(nn.Module):
     """Decoder + LM head; forward(input_ids, past_key_values, logits_to_keep) runs one
-    prefill chunk (the reference runtime's call, chunked_prefill_runtime.py:1168-1203)."""
+    prefill chunk (the reference runtime's call, chunked_prefill_runtime.py:1168-1203) or,
+    with fewer than 64 tokens or after an unaligned step, one dense decode step."""
 
     attn_cls: Type[nn.Module] = nn.Module
     cache_with_kmean = False
@@ -189,8 +216,6 @@ class CompactAttnLlamaForCausalLM(nn.Module):
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, past_key_values: ChunkedPrefillCache,
                 logits_to_keep: int = 1) -> torch.Tensor:
-        if input_ids.shape[1] < 2:
-            raise ValueError("decode steps (one token) are not supported by the compactattn prefill path")
         h = self.model(input_ids, past_key_values)
         if logits_to_keep > 0:
             h = h[:, -logits_to_keep:]

@@ -32,7 +32,8 @@ from ... import ops
 from ...modules._core import COMPACTATTN_VERSION
 from ..attn_gate import AttnGate
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
-from .modeling_llama_common import ChunkedPrefillCache, CompactAttnLlamaForCausalLM, apply_rotary_pos_emb
+from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, apply_rotary_pos_emb,
+                                     dense_decode_forward, is_decode_step)
 
 BLOCK = 64
 
@@ -110,6 +111,10 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
             raise ValueError("padded positions are not supported by the compactattn prefill path")
         if block_position_embeddings is None:
             raise ValueError("block_position_embeddings (per-block rotary tables) are required")
+        if is_decode_step(hidden_states, past_key_value.layer(self.layer_idx)):
+            out = dense_decode_forward(self, hidden_states, position_embeddings, past_key_value.layer(self.layer_idx))
+            self._compactattn_last_stats = {"path": "decode_dense"} if self.compactattn_debug else None
+            return out, 0.0, None, None, None
         B, L, _ = hidden_states.shape
         if L % BLOCK:
             raise ValueError("chunk lengths must be multiples of 64 tokens")

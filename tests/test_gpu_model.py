@@ -108,6 +108,30 @@ def test_seer_keep_all_equals_dense(gpu):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("cls", [SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaFlashPrefillCompactAttnForCausalLM])
+def test_decode_steps_match_fp32_reference(gpu, cls):
+    """Dense chunked prefill, then decode steps of 1, 5 and 1 tokens from an unaligned cache
+    length: each step's last logits match the fp32 CPU forward over the whole sequence."""
+    print(f"case: model decode {cls.__name__}", flush=True)
+    m = _model(cls, gpu, seerattn_chunked_prefill_force_dense=True)
+    ids = synthetic_prompt(1, T + 7, m.config.vocab_size, 4321, gpu)
+    cache = m.new_cache(1, T + 64)
+    for s0 in range(0, T, CHUNK):
+        m(ids[:, s0:s0 + CHUNK], cache)
+    pos = T
+    for n in (1, 5, 1):
+        logits = m(ids[:, pos:pos + n], cache)
+        pos += n
+        assert cache.get_seq_length() == pos
+        ref = _reference_logits(m, ids[:, :pos])
+        got = logits.float().cpu()
+        cos = F.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item()
+        assert cos > 0.999, (n, cos)
+        assert (got - ref).abs().max().item() <= 0.05 * ref.abs().max().item()
+    with pytest.raises(ValueError, match="at most 64"):  # after decode steps every call is a decode step
+        m(ids[:, :128], cache)
+
+
 def _capture_layer_inputs(model, layer_idx):
     captured = []
     attn = model.model.layers[layer_idx].self_attn

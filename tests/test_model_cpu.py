@@ -71,11 +71,30 @@ def test_rope_matches_rotate_half_formula():
     assert torch.equal(bc[2], m.model.rotary_emb.cos[128])
 
 
-def test_forward_rejects_decode_and_cpu():
+def test_forward_rejects_cpu_tensors_for_prefill_and_decode():
+    """The HIP path has no CPU fallback: a CPU model fails loudly in both prefill chunks and
+    decode steps."""
     m = SeerAttnLlamaChunkedDenseForCausalLM(tiny())
     ids = synthetic_prompt(1, 128, 64, 0, "cpu")
-    with pytest.raises(ValueError, match="decode"):
-        m(ids[:, :1], None)
-    cache = m.new_cache(1, 128)
+    cache = m.new_cache(1, 192)
     with pytest.raises(ValueError, match="GPU tensor"):
         m(ids, cache)
+    cache = m.new_cache(1, 192)
+    with pytest.raises(ValueError, match="GPU tensor"):
+        m(ids[:, :1], cache)
+
+
+def test_paged_cache_decode_append_rules():
+    from compactattention_amd.kv_cache import PagedKVCache
+
+    c = PagedKVCache(1, 2, 192, "cpu")
+    k = torch.randn((1, 64, 2, 128)).to(torch.bfloat16)
+    c.length = 64  # as after one prefill chunk
+    start = c.append_tokens(k[:, :3], k[:, :3])
+    assert start == 64 and c.length == 67
+    assert torch.equal(c.k[0, :, 64:67], k[0, :3].transpose(0, 1))
+    with pytest.raises(ValueError, match="partial block"):
+        c.append(k, k)
+    with pytest.raises(ValueError, match="capacity"):
+        c.append_tokens(torch.zeros((1, 126, 2, 128), dtype=torch.bfloat16),
+                        torch.zeros((1, 126, 2, 128), dtype=torch.bfloat16))
