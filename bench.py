@@ -434,8 +434,23 @@ def decode_lines(dev, hq=32, hkv=8):
                       "hbm_frac": round(kv_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)})
         del k, v, q, K, V, out, ws
         torch.cuda.empty_cache()
+    # practical HBM reference on the same part: a 1 GiB device-to-device copy (read + write)
+    src = torch.empty((1 << 29,), dtype=torch.int16, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(10):
+        dst.copy_(src)
+    b_.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * src.numel() * 2 * 10 / (a.elapsed_time(b_) * 1e-3) / 1e9
+    del src, dst
+    torch.cuda.empty_cache()
     return {"workload": f"dense decode, 1 query token per request, {hq} Q / {hkv} KV heads, d 128, bf16 cache; "
-                        "per-request split plan + LSE merge", "lines": lines}
+                        "per-request split plan + LSE merge", "lines": lines,
+            "device_copy_gbps": round(copy_gbps, 1)}
 
 
 def measured_traffic():
