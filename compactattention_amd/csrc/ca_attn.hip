@@ -91,6 +91,24 @@ __device__ __forceinline__ lds_void_t* to_lds(const uint8_t* p) {
 __device__ __forceinline__ lds_i16x4_t* to_lds_v4(const uint8_t* p) {
     return (lds_i16x4_t*)(p);
 }
+// max(x, x of lane ^ 32): v_permlane32_swap hands each half the other half's values, so
+// the max of its two outputs is the pair's max in every lane (no LDS round trip).
+__device__ __forceinline__ float xor32_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// max(x, x of lane ^ 16), the same way with v_permlane16_swap
+__device__ __forceinline__ float xor16_max(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Wave-uniform reads of tables the kernel never writes (block ids, counts, page tables) go
+// through the scalar data cache: s_load waits on lgkmcnt, so they do not queue behind the
+// LDS-DMA loads in flight on vmcnt.
+typedef const __attribute__((address_space(4))) int32_t const_i32_t;
+__device__ __forceinline__ int32_t sload(const int32_t* p) {
+    return *(const_i32_t*)p;
+}
 // Completes this wave's outstanding LDS-DMA loads (vector-memory counter).
 __device__ __forceinline__ void wait_dma() {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -150,12 +168,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // Table entries are clamped into [0, nkb) so a corrupt table cannot address outside the
     // KV tensors.
     const int32_t* tab = kTab ? p.table + (int64_t)row * p.table_stride : nullptr;
-    auto block_id = [&](int e) { return kTab ? min(max(tab[e], 0), nkb - 1) : e; };
+    auto block_id = [&](int e) { return kTab ? min(max(sload(tab + e), 0), nkb - 1) : e; };
     const int lim = (qpos0 + t_last) >> 6;  // last block the tile can see
     int n_vis;
     if (kTab) {
-        n_vis = min(max(p.counts[row], 0), s.cap);
-        while (n_vis > 0 && tab[n_vis - 1] > lim) --n_vis;
+        n_vis = min(max(sload(p.counts + row), 0), s.cap);
+        while (n_vis > 0 && sload(tab + n_vis - 1) > lim) --n_vis;
     } else {
         n_vis = min(nkb, lim + 1);
     }
@@ -230,8 +248,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int kv_tokens = qpos0 + s.Lq;
     auto issue_block = [&](int e, int stage) {
         const int kb = block_id(e);
-        const int64_t kphys = kpt ? kpt[kb] : kb;
-        const int64_t vphys = vpt ? vpt[kb] : kb;
+        const int64_t kphys = kpt ? sload(kpt + kb) : kb;
+        const int64_t vphys = vpt ? sload(vpt + kb) : kb;
         const int rows = min(kv_tokens - kb * 64, 64);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(kbase_row + kphys * p.k.sblk), 0, rows * kstok_b, 0x00020000);
@@ -274,15 +292,24 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.0f;
-        // the two 32-key accumulators alternate so consecutive MFMAs are independent
+        // the two 32-key accumulators alternate so consecutive MFMAs are independent; the
+        // K fragment reads run six ahead of the MFMAs (scheduling groups below)
         __builtin_amdgcn_s_setprio(1);
+        {
+            bf16x8_t kfr[16];
 #pragma unroll
-        for (int ds = 0; ds < 8; ++ds)
+            for (int i = 0; i < 16; ++i) kfr[i] = *reinterpret_cast<const bf16x8_t*>(ks + k_off[i >> 1] + (i & 1) * 8192);
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + k_off[ds] + kt * 8192);
-                sacc[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[ds], sacc[kt], 0, 0, 0);
+            for (int i = 0; i < 16; ++i)
+                sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[i], qf[i >> 1], sacc[i & 1], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // 6 LDS reads
+#pragma unroll
+            for (int i = 0; i < 10; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
             }
+            __builtin_amdgcn_sched_group_barrier(0x008, 6, 0);
+        }
         __builtin_amdgcn_s_setprio(0);
         if (masked) {
             // value j of half kt holds key kt*32 + swap23(8*(j/4) + 4*h + j%4)
@@ -301,7 +328,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sacc[kt][j]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+        mx = xor32_max(mx) * sl2;
         float alpha = 1.0f;
         if (mx > m_run + kRescale) {
             alpha = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when m_run = -inf
@@ -594,7 +621,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams 
     u32x4_t kf[2][2][4];
     uint8_t* vhalf[2] = {vbuf, vbuf + kDecVBytes / 2};
     auto block_rsrc = [&](const uint16_t* base, const int32_t* pt, int64_t sblk, int kb, int stok_b) {
-        const int64_t phys = pt ? pt[kb] : kb;
+        const int64_t phys = pt ? sload(pt + kb) : kb;
         const int rows = min(kv_tokens - kb * 64, 64);
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + phys * sblk), 0, rows * stok_b,
                                                  0x00020000);
@@ -654,8 +681,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams 
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[kt][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+        mx = xor32_max(xor16_max(mx)) * sl2;
         float alpha = 1.0f;
         if (mx > m_run + kRescale) {
             alpha = __builtin_amdgcn_exp2f(m_run - mx);
