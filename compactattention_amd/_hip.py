@@ -40,6 +40,7 @@ EXPORTED = (
     "ca_union_compact",
     "ca_compact_keep_kv",
     "ca_dense_table",
+    "ca_table_to_csr",
     "ca_attn_fwd",
     "ca_attn_workspace_size",
     "ca_attn_pick_splits",
@@ -117,6 +118,7 @@ _SIGNATURES = {
     "ca_union_compact": (ctypes.c_int, [_P(Dims), _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "ca_compact_keep_kv": (ctypes.c_int, [_P(Dims), _vp, _vp, _vp, _i64, _vp, _vp]),
     "ca_dense_table": (ctypes.c_int, [_P(Dims), _vp, _vp, _i64, _vp, _vp]),
+    "ca_table_to_csr": (ctypes.c_int, [_P(Dims), _vp, _i64, _vp, _vp, _vp, _i64, _vp, _vp]),
     "ca_attn_fwd": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(KvLayout), _P(KvLayout), _vp, _i64, _vp, _vp,
                                    _f32, _P(SeqLayout), _vp, _i32, _vp, _i64, _vp]),
     "ca_attn_workspace_size": (ctypes.c_int64, [_P(Dims), _vp, _i32]),

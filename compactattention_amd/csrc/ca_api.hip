@@ -315,6 +315,29 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
     return ok();
 }
 
+int ca_table_to_csr(const ca_dims* dims, const int32_t* table, int64_t table_stride, const int32_t* counts,
+                    int32_t* kv_indptr, int32_t* kv_indices, int64_t indices_capacity, int32_t* kv_last_page_len,
+                    void* stream) {
+    if (dims == nullptr) return fail(CA_ERR_INVALID, "dims is NULL");
+    if (dims->batch < 1 || dims->num_kv_heads < 1 || dims->kv_cap < 1)
+        return fail(CA_ERR_INVALID, "batch, num_kv_heads and kv_cap must be positive");
+    const int64_t rows = (int64_t)dims->batch * dims->num_kv_heads;
+    if (rows > ca::kCsrRowsMax) return fail(CA_ERR_LIMIT, "rows=%lld > %d", (long long)rows, ca::kCsrRowsMax);
+    if ((int64_t)dims->kv_cap * rows >= ((int64_t)1 << 31))
+        return fail(CA_ERR_LIMIT, "rows * kv_cap must stay below 2^31 (int32 page ids)");
+    if (table == nullptr || counts == nullptr || kv_indptr == nullptr || kv_indices == nullptr)
+        return fail(CA_ERR_INVALID, "table, counts, kv_indptr and kv_indices are required");
+    if (table_stride < dims->kv_cap)
+        return fail(CA_ERR_INVALID, "table_stride=%lld < kv_cap=%d", (long long)table_stride, dims->kv_cap);
+    if (indices_capacity < rows * dims->kv_cap)
+        return fail(CA_ERR_INVALID, "indices_capacity=%lld < rows * kv_cap=%lld (the counts are not known on the host)",
+                    (long long)indices_capacity, (long long)(rows * dims->kv_cap));
+    hipError_t e = ca::launch_table_csr(table, table_stride, counts, static_cast<int>(rows), dims->kv_cap, kv_indptr,
+                                        kv_indices, kv_last_page_len, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "table_to_csr launch");
+    return ok();
+}
+
 int32_t ca_attn_pick_splits(const ca_dims* dims, const int32_t* past_blocks_host) {
     ca::Shape s;
     ca::PastBlocks pb;

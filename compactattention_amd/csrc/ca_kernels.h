@@ -47,6 +47,9 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
                                uint32_t* rowmask, float* scores_out, hipStream_t stream);
 
 size_t union_lds_bytes(const Shape& s);
+constexpr int kCsrRowsMax = 8192;
+hipError_t launch_table_csr(const int32_t* table, int64_t table_stride, const int32_t* counts, int rows, int cap,
+                            int32_t* indptr, int32_t* indices, int32_t* last_page_len, hipStream_t stream);
 
 hipError_t launch_union_compact(const Shape& s, const uint32_t* rowmask, int last_n_block,
                                 const uint8_t* keep_kv_in, const PastBlocks& pb, uint8_t* keep_block,

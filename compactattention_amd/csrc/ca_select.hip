@@ -697,6 +697,67 @@ __global__ __launch_bounds__(256) void union_compact_kernel(UnionParams p) {
     if (t == 0) p.counts[row] = total;
 }
 
+// ---------------------------------------------------------------------------------------
+// Block tables -> CSR page lists (FlashInfer's paged-KV form): kv_indptr[r] is the exclusive
+// prefix sum of the row counts, kv_indices[kv_indptr[r] + i] = r * kv_cap + table[r][i] (the
+// global page id of the heads-first cache), kv_last_page_len[r] = 64.  One workgroup: the
+// rows are scanned 1024 at a time, then each wave copies whole rows.
+struct CsrParams {
+    const int32_t* table;
+    int64_t table_stride;
+    const int32_t* counts;
+    int rows;
+    int cap;
+    int32_t* indptr;
+    int32_t* indices;
+    int32_t* last_page_len;
+};
+
+constexpr int kCsrThreads = 1024;
+constexpr int kCsrMaxRows = 8192;
+
+__global__ __launch_bounds__(kCsrThreads) void table_csr_kernel(CsrParams p) {
+    __shared__ int32_t off[kCsrMaxRows + 1];
+    __shared__ int32_t wsum[kCsrThreads / 64];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wv = t >> 6;
+    int carry = 0;
+    for (int base = 0; base < p.rows; base += kCsrThreads) {
+        const int r = base + t;
+        const int c = r < p.rows ? min(max(p.counts[r], 0), p.cap) : 0;
+        // inclusive scan inside the wave
+        int x = c;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int y = __shfl_up(x, o, 64);
+            if (lane >= o) x += y;
+        }
+        if (lane == 63) wsum[wv] = x;
+        __syncthreads();
+        int before = carry;
+        for (int v = 0; v < wv; ++v) before += wsum[v];
+        int total = carry;
+        for (int v = 0; v < kCsrThreads / 64; ++v) total += wsum[v];
+        if (r < p.rows) off[r] = before + x - c;
+        __syncthreads();  // wsum is rewritten by the next chunk
+        carry = total;
+    }
+    if (t == 0) off[p.rows] = carry;
+    __syncthreads();
+    for (int r = t; r <= p.rows; r += kCsrThreads) p.indptr[r] = off[r];
+    if (p.last_page_len)
+        for (int r = t; r < p.rows; r += kCsrThreads) p.last_page_len[r] = 64;
+    for (int r = wv; r < p.rows; r += kCsrThreads / 64) {
+        const int c = off[r + 1] - off[r];
+        const int32_t* src = p.table + (int64_t)r * p.table_stride;
+        int32_t* dst = p.indices + off[r];
+        const int gbase = r * p.cap;
+        for (int i = lane; i < c; i += 64) dst[i] = gbase + min(max(src[i], 0), p.cap - 1);
+    }
+}
+
+
 }  // namespace
 
 hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr& v_new,
@@ -753,6 +814,21 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
         hipLaunchKernelGGL(row_select_kernel<true>, grid, dim3(kSelThreads), lds, stream, p);
     else
         hipLaunchKernelGGL(row_select_kernel<false>, grid, dim3(kSelThreads), lds, stream, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_table_csr(const int32_t* table, int64_t table_stride, const int32_t* counts, int rows, int cap,
+                            int32_t* indptr, int32_t* indices, int32_t* last_page_len, hipStream_t stream) {
+    CsrParams p;
+    p.table = table;
+    p.table_stride = table_stride;
+    p.counts = counts;
+    p.rows = rows;
+    p.cap = cap;
+    p.indptr = indptr;
+    p.indices = indices;
+    p.last_page_len = last_page_len;
+    hipLaunchKernelGGL(table_csr_kernel, dim3(1), dim3(kCsrThreads), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -286,6 +286,26 @@ def dense_table(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv
     return table, counts
 
 
+def table_to_csr(table: torch.Tensor, counts: torch.Tensor, batch: int, num_kv_heads: int, kv_cap: int,
+                 with_last_page_len: bool = False):
+    """Block tables -> (kv_indptr [rows+1], kv_indices [rows*kv_cap] (first kv_indptr[-1] valid),
+    kv_last_page_len [rows] or None), the paged-KV CSR form of
+    build_flashinfer_kv_indices (compact_attn/csrc/compactattn/cache_fill_kernel.cu:485-505)."""
+    _need_cuda("table", table, torch.int32)
+    _need_cuda("counts", counts, torch.int32)
+    rows = batch * num_kv_heads
+    if table.dim() != 2 or table.stride(1) != 1 or table.shape[0] < rows:
+        raise ValueError("table must be [B*Hkv, >= kv_cap] with contiguous rows")
+    d = make_dims(batch, BLOCK, num_kv_heads, num_kv_heads, kv_cap)
+    dev = table.device
+    indptr = torch.empty((rows + 1,), dtype=torch.int32, device=dev)
+    indices = torch.empty((rows * kv_cap,), dtype=torch.int32, device=dev)
+    last = torch.empty((rows,), dtype=torch.int32, device=dev) if with_last_page_len else None
+    check(_hip.lib().ca_table_to_csr(ctypes.byref(d), table.data_ptr(), table.stride(0), counts.data_ptr(),
+                                     indptr.data_ptr(), indices.data_ptr(), indices.numel(), _ptr(last), _stream()))
+    return indptr, indices, last
+
+
 def attn_workspace_bytes(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int, kv_cap: int,
                          num_splits: int = 0) -> int:
     d = make_dims(len(past_blocks), q_len, num_q_heads, num_kv_heads, kv_cap)

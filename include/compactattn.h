@@ -165,7 +165,7 @@ int ca_select_scores(const ca_dims* dims, const void* scores, int32_t dtype, int
  * Replaces: _build_kv_head_union_keep_block_mask (attention_forward_chunked_dense.py:
  * 641-683), build_past_indices_and_metadata_from_keep_block / build_block_table /
  * build_selected_indices_from_kv_keep_block / build_flashinfer_kv_indices
- * (cache_fill_kernel.cu:163-190,328-505) and the Triton union kernel
+ * (cache_fill_kernel.cu:163-190,328-483; the CSR form is ca_table_to_csr) and the Triton union kernel
  * (flashprefill_prefill.py:307-376).
  */
 int ca_union_compact(const ca_dims* dims, const uint32_t* rowmask, int32_t last_n_block,
@@ -181,6 +181,22 @@ int ca_union_compact(const ca_dims* dims, const uint32_t* rowmask, int32_t last_
  */
 int ca_compact_keep_kv(const ca_dims* dims, const uint8_t* keep_kv, const int32_t* past_blocks_host,
                        int32_t* table, int64_t table_stride, int32_t* counts, void* stream);
+
+/*
+ * Block tables -> CSR page lists for FlashInfer-style paged-KV consumers: kv_indptr
+ * [B*Hkv + 1] (exclusive prefix sum of counts), kv_indices (kv_indices[kv_indptr[r] + i] =
+ * r * kv_cap + table[r][i], the global page id of row r's block in the heads-first cache;
+ * room for B*Hkv*kv_cap entries since the counts are device data), and optionally
+ * kv_last_page_len [B*Hkv] (= 64, every page is full).  Uses dims->batch, num_kv_heads and
+ * kv_cap only.  At most 8192 rows.
+ * Replaces: the pages_per_row / kv_indptr / kv_indices construction of
+ * build_flashinfer_kv_indices (compact_attn/csrc/compactattn/cache_fill_kernel.cu:485-505) and
+ * its torch spec _build_index_metadata_reference_from_keep_block_kv
+ * (compact_attn/kernels/varlen/flashinfer_zero_copy_prefill.py:482-510).
+ */
+int ca_table_to_csr(const ca_dims* dims, const int32_t* table, int64_t table_stride, const int32_t* counts,
+                    int32_t* kv_indptr, int32_t* kv_indices, int64_t indices_capacity, int32_t* kv_last_page_len,
+                    void* stream);
 
 /* Identity tables (every block 0..P_b+Qb-1): the dense full-KV comparator's input. */
 int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t* table,

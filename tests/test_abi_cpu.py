@@ -134,6 +134,19 @@ def test_decode_layout_and_workspace_validation():
     assert lib.ca_attn_decode_workspace_size(ctypes.byref(d1), _past(64), 0) == 0
 
 
+def test_table_to_csr_validation():
+    lib = _hip.lib()
+    d = _dims(batch=2, num_kv_heads=2, kv_cap=10)
+    call = lambda stride, cap_idx, dd=d: lib.ca_table_to_csr(ctypes.byref(dd), FAKE, stride, FAKE, FAKE, FAKE,  # noqa: E731
+                                                            cap_idx, None, None)
+    assert call(9, 40) == _hip.CA_ERR_INVALID and "table_stride" in _hip.last_error()
+    assert call(10, 39) == _hip.CA_ERR_INVALID and "indices_capacity" in _hip.last_error()
+    big = _dims(batch=64, num_kv_heads=129, kv_cap=10)
+    assert call(10, 1 << 30, big) == _hip.CA_ERR_LIMIT
+    rc = lib.ca_table_to_csr(ctypes.byref(d), None, 10, FAKE, FAKE, FAKE, 40, None, None)
+    assert rc == _hip.CA_ERR_INVALID
+
+
 def test_rule_and_select_validation():
     lib = _hip.lib()
     d = _dims()

@@ -244,6 +244,33 @@ def test_dense_table(gpu):
             assert (t[r, P + 2:] == -1).all()
 
 
+@pytest.mark.parametrize("B,Hkv,cap", [(3, 2, 40), (1, 8, 2064), (2, 3, 7)])
+def test_table_to_csr_matches_reference_spec(gpu, B, Hkv, cap):
+    """CSR page lists from the block tables equal the reference's torch spec applied to the
+    keep mask itself (flashinfer_zero_copy_prefill.py:482-510): pages_per_row = keep.sum,
+    kv_indptr = [0, cumsum], kv_indices = global_ids[keep] with global id row*cap + block."""
+    _print_case(test="table_to_csr", B=B, Hkv=Hkv, cap=cap)
+    g = torch.Generator().manual_seed(B * 100 + cap)
+    qb = 1
+    past = [int(x) for x in torch.randint(0, cap - qb + 1, (B,), generator=g)]
+    keep_kv = (torch.rand((B, Hkv, cap), generator=g) < 0.3).to(torch.uint8)
+    table, counts = ops.compact_keep_kv(keep_kv.to(gpu), past, 64 * qb, Hkv, cap)
+    indptr, indices, last = ops.table_to_csr(table, counts, B, Hkv, cap, with_last_page_len=True)
+    torch.cuda.synchronize()
+    keep = keep_kv.numpy().astype(bool).copy()
+    for b, P in enumerate(past):  # visible blocks: the past's selection + the chunk's blocks
+        keep[b, :, P + qb:] = False
+        keep[b, :, P:P + qb] = True
+    keep_flat = keep.reshape(B * Hkv, cap)
+    ref_ptr = np.concatenate([[0], np.cumsum(keep_flat.sum(axis=1))]).astype(np.int32)
+    global_ids = np.arange(B * Hkv * cap, dtype=np.int32).reshape(B * Hkv, cap)
+    ref_idx = global_ids[keep_flat]
+    got_ptr = indptr.cpu().numpy()
+    assert np.array_equal(got_ptr, ref_ptr)
+    assert np.array_equal(indices.cpu().numpy()[:ref_ptr[-1]], ref_idx)
+    assert (last.cpu().numpy() == 64).all()
+
+
 # ----------------------------------------------------------------------------- attention
 def _attn_case(gpu, past_tokens, Lq, Hq, Hkv, layout, splits, keep_frac, seed):
     ch = make_chunk(past_tokens, Lq, Hq, Hkv, seed=seed, planted_blocks=2)
