@@ -13,19 +13,27 @@ from typing import Optional, Tuple
 
 import torch
 
-from .prefill_sparse.llama.modeling_llama_common import ChunkedPrefillCache, CompactAttnLlamaForCausalLM
+from .prefill_sparse.llama.modeling_llama_common import ChunkedPrefillCache
 
 
 @torch.no_grad()
-def run_chunked_prefill_once(model: CompactAttnLlamaForCausalLM, input_ids: torch.Tensor, chunk_size: int,
+def run_chunked_prefill_once(model: torch.nn.Module, input_ids: torch.Tensor, chunk_size: int,
                              cache: Optional[ChunkedPrefillCache] = None) -> Tuple[torch.Tensor, float]:
     B, T = input_ids.shape
     if chunk_size <= 0 or chunk_size % 64:
         raise ValueError("chunk_size must be a positive multiple of 64")
     if T % 64:
         raise ValueError("the prompt length must be a multiple of 64 tokens")
+    # a stock transformers model whose attention was replaced (load_attention_replacement)
+    # takes the cache as past_key_values and returns a model output
+    hf = getattr(getattr(model, "config", None), "seerattn_attention_harness", None) == "replacement"
     if cache is None:
-        cache = model.new_cache(B, T)
+        if hf:
+            from .load_attention_replacement import new_compactattn_cache
+
+            cache = new_compactattn_cache(model, B, T)
+        else:
+            cache = model.new_cache(B, T)
     else:
         cache.reset()
     logits = None
@@ -33,7 +41,11 @@ def run_chunked_prefill_once(model: CompactAttnLlamaForCausalLM, input_ids: torc
     t0 = time.perf_counter()
     for start in range(0, T, chunk_size):
         end = min(start + chunk_size, T)
-        logits = model(input_ids[:, start:end], cache, logits_to_keep=1)
+        if hf:
+            logits = model(input_ids=input_ids[:, start:end], past_key_values=cache, use_cache=True,
+                           logits_to_keep=1).logits
+        else:
+            logits = model(input_ids[:, start:end], cache, logits_to_keep=1)
     torch.cuda.synchronize()
     return logits, time.perf_counter() - t0
 

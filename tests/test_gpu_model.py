@@ -132,6 +132,55 @@ def test_decode_steps_match_fp32_reference(gpu, cls):
         m(ids[:, :128], cache)
 
 
+@pytest.mark.parametrize("variant", ["seer_compactattn", "flashprefill_compactattn"])
+def test_hf_replacement_matches_stock_model(gpu, variant):
+    """A stock transformers Llama with its attention replaced (dense chunks, then decode steps)
+    matches the same stock model run in fp32 on the CPU with its own attention."""
+    import copy
+
+    transformers = pytest.importorskip("transformers")
+    from compactattention_amd.load_attention_replacement import (load_llama_attention_replacement_model,
+                                                                 new_compactattn_cache)
+
+    print(f"case: hf replacement {variant}", flush=True)
+    cfg = transformers.LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+                                   max_position_embeddings=2048)
+    torch.manual_seed(11)
+    stock = transformers.LlamaForCausalLM(cfg).eval()
+    ref_model = copy.deepcopy(stock).float()
+    model = load_llama_attention_replacement_model(base_model=stock.to(gpu), variant=variant)
+    model.compactattn_config.seerattn_chunked_prefill_force_dense = True
+    ids = synthetic_prompt(1, T + 6, cfg.vocab_size, 77, gpu)
+    cache = new_compactattn_cache(model, 1, T + 64)
+
+    def check(logits, upto):
+        with torch.no_grad():
+            ref = ref_model(input_ids=ids[:, :upto].cpu()).logits[:, -1:].float()
+        got = logits.float().cpu()
+        cos = F.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item()
+        assert cos > 0.999, (upto, cos)
+        assert (got - ref).abs().max().item() <= 0.05 * ref.abs().max().item()
+
+    logits, _ = run_chunked_prefill_once(model, ids[:, :T], CHUNK, cache)
+    check(logits, T)
+    pos = T
+    for n in (1, 5):
+        with torch.no_grad():
+            logits = model(input_ids=ids[:, pos:pos + n], past_key_values=cache, use_cache=True,
+                           logits_to_keep=1).logits
+        pos += n
+        check(logits, pos)
+    # the selecting path runs through the same adapter: later chunks select blocks
+    model.compactattn_config.seerattn_chunked_prefill_force_dense = False
+    for layer in model.model.layers:
+        layer.self_attn.compactattn_debug = True
+    logits, _ = run_chunked_prefill_once(model, ids[:, :T], CHUNK, cache)
+    assert torch.isfinite(logits.float()).all()
+    stats = model.model.layers[1].self_attn._compactattn_last_stats
+    assert stats["path"] in ("chunked_selected", "flashprefill_chunked_selected")
+
+
 def _capture_layer_inputs(model, layer_idx):
     captured = []
     attn = model.model.layers[layer_idx].self_attn
