@@ -390,7 +390,7 @@ def ragged_batch(dev, pasts=(16384, 49152, 98304, 131072), chunk=512, hq=28, hkv
         "attn_speedup_vs_dense": round(dense_us / attn_us, 3),
         "keep_ratio": round(keep_of(counts), 4),
         "topk_per_row": topk,
-        "attn_splits": "per request, max %d" % splits,
+        "attn_splits": splits,
         "tok_per_s": round(B * chunk / (path_us * 1e-6), 1),
     }
 

@@ -327,9 +327,8 @@ def attn_pick_splits(past_blocks: Sequence[int], q_len: int, num_q_heads: int, n
 def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.Tensor, past_blocks: Sequence[int],
              scale: float, kv_cap: int, num_kv_heads: int, out: Optional[torch.Tensor] = None, with_lse: bool = False,
              num_splits: int = 0, workspace: Optional[torch.Tensor] = None):
-    """Indexed attention prefill; q/out [B, Lq, Hq, 128] bf16.  num_splits = 0 splits each
-    request's block list by the library's per-request plan; a positive value splits every
-    row that many ways."""
+    """Indexed attention prefill; q/out [B, Lq, Hq, 128] bf16.  num_splits = 0 lets the
+    library pick the split count; a positive value splits every row that many ways."""
     B, Lq, Hq, _ = q.shape
     ql = seq_layout(q, "q")
     if out is None:
@@ -341,7 +340,7 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
         raise ValueError("table must be [B*Hkv, >= kv_cap] with contiguous rows")
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     pa = past_array(past_blocks)
-    # num_splits = 0 hands the library its per-request split plan
+    # num_splits = 0 hands the choice to the library
     need = _hip.lib().ca_attn_workspace_size(ctypes.byref(d), pa, int(num_splits))
     if need < 0:
         raise _hip.CaError(int(need), _hip.last_error())

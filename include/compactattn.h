@@ -208,9 +208,10 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
  * keys of the blocks table[row][0..counts[row]) of row = b*Hkv + h/G with bottom-right
  * causal masking (key position j visible iff j <= 64*P_b + t).  out has q's layout;
  * lse (optional, [B, Hq, q_len] fp32, natural log) receives the log-sum-exp.
- * num_splits >= 1 splits every row's block list that many ways; num_splits = 0 plans the
- * splits per request, in proportion to its blocks (P_b + q_len/64), so the work items of a
- * ragged batch carry similar amounts of work.  More than one split needs a workspace of
+ * num_splits >= 1 splits every row's block list that many ways; num_splits = 0 picks one
+ * count for the launch, sized to about 512 work items (row tiles x splits) with at least
+ * ~16 blocks per split (ca_attn_pick_splits).  Whole KV rows are placed on the XCDs
+ * longest-first either way.  More than one split needs a workspace of
  * ca_attn_workspace_size(dims, past, num_splits) bytes.
  * Replaces: flash_attn_with_kvcache / FlashInfer paged prefill as driven by
  * flash_attn_indexed_prefill_from_paged_kv (compact_attn/kernels/varlen/
@@ -225,11 +226,11 @@ int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout*
                 const ca_seq_layout* out, float* lse, int32_t num_splits, void* workspace,
                 int64_t workspace_bytes, void* stream);
 
-/* Workspace bytes ca_attn_fwd needs for num_splits (0 = its per-request plan). */
+/* Workspace bytes ca_attn_fwd needs for num_splits (0 = the automatic count). */
 int64_t ca_attn_workspace_size(const ca_dims* dims, const int32_t* past_blocks_host,
                                int32_t num_splits);
 
-/* The largest per-request split count of ca_attn_fwd's plan for num_splits = 0. */
+/* The split count ca_attn_fwd uses for num_splits = 0. */
 int32_t ca_attn_pick_splits(const ca_dims* dims, const int32_t* past_blocks_host);
 
 /*

@@ -329,8 +329,8 @@ def test_attention_ragged_batch(gpu):
 
 
 def test_attention_ragged_split_plan(gpu):
-    """Automatic split-KV plans split each request in proportion to its blocks: here the
-    four requests get 1, 3, 7 and 12 splits, so the merge skips the single-split rows."""
+    """The automatic split count (here 12 for every request, the shortest request's lists
+    being split down to a few blocks) through the LSE merge."""
     _print_case(test="attention_ragged_plan")
     _attn_case(gpu, [64 * 16, 64 * 60, 64 * 120, 64 * 200], 128, 8, 2, "heads_first", 0, 0.3, seed=43)
 
