@@ -46,6 +46,9 @@ EXPORTED = (
     "ca_attn_pick_splits",
     "ca_attn_decode",
     "ca_attn_decode_workspace_size",
+    "ca_rope_apply",
+    "ca_rmsnorm",
+    "ca_swiglu",
 )
 
 
@@ -126,6 +129,9 @@ _SIGNATURES = {
     "ca_attn_decode": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(KvLayout), _P(KvLayout), _vp, _f32,
                                       _P(SeqLayout), _vp, _i32, _vp, _i64, _vp]),
     "ca_attn_decode_workspace_size": (ctypes.c_int64, [_P(Dims), _vp, _i32]),
+    "ca_rope_apply": (ctypes.c_int, [_P(SeqLayout), _P(SeqLayout), _i32, _i32, _i32, _vp, _vp, _vp]),
+    "ca_rmsnorm": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp, _i64, _i64, _i32, _f32, _vp]),
+    "ca_swiglu": (ctypes.c_int, [_vp, _i64, _vp, _i64, _vp, _i64, _i64, _i32, _vp]),
 }
 
 _lib: Optional[ctypes.CDLL] = None

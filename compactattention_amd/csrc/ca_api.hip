@@ -437,3 +437,58 @@ int ca_attn_decode(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layo
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------------------
+// Model plumbing: fused element-wise kernels of the Llama integration.
+
+int ca_rope_apply(const ca_seq_layout* x, const ca_seq_layout* y, int32_t batch, int32_t len, int32_t heads,
+                  const float* cos, const float* sin, void* stream) {
+    ca::SeqAddr xa, ya;
+    int rc;
+    if ((rc = check_seq(x, "x", &xa)) != CA_OK) return rc;
+    if ((rc = check_seq(y, "y", &ya)) != CA_OK) return rc;
+    if (batch < 1 || len < 1 || heads < 1) return fail(CA_ERR_INVALID, "batch, len and heads must be positive");
+    if ((int64_t)batch * len * heads * 16 >= ((int64_t)1 << 40)) return fail(CA_ERR_LIMIT, "too many rows");
+    if (cos == nullptr || sin == nullptr) return fail(CA_ERR_INVALID, "cos and sin are required");
+    hipError_t e = ca::launch_rope(xa, ya, cos, sin, batch, len, heads, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "rope launch");
+    return ok();
+}
+
+int ca_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride, uint16_t* sum_out,
+               int64_t s_stride, const uint16_t* w, uint16_t* y, int64_t y_stride, int64_t rows, int32_t n, float eps,
+               void* stream) {
+    if (x == nullptr || w == nullptr || y == nullptr) return fail(CA_ERR_INVALID, "x, w and y are required");
+    if (!aligned16(x) || !aligned16(w) || !aligned16(y)) return fail(CA_ERR_INVALID, "x, w and y must be 16-byte aligned");
+    if (n < 8 || n % 8 || x_stride % 8 || y_stride % 8 || x_stride < n || y_stride < n)
+        return fail(CA_ERR_INVALID, "n=%d must be a positive multiple of 8 and the row strides multiples of 8 >= n", n);
+    if ((residual == nullptr) != (sum_out == nullptr))
+        return fail(CA_ERR_INVALID, "residual and sum_out are given together or not at all");
+    if (residual != nullptr) {
+        if (!aligned16(residual) || !aligned16(sum_out))
+            return fail(CA_ERR_INVALID, "residual and sum_out must be 16-byte aligned");
+        if (r_stride % 8 || s_stride % 8 || r_stride < n || s_stride < n)
+            return fail(CA_ERR_INVALID, "residual / sum_out row strides must be multiples of 8 >= n");
+    }
+    if (rows < 0 || rows >= ((int64_t)1 << 31)) return fail(CA_ERR_LIMIT, "rows=%lld outside [0, 2^31)", (long long)rows);
+    if (!(eps >= 0.0f)) return fail(CA_ERR_INVALID, "eps must be >= 0");
+    if (rows == 0) return ok();
+    hipError_t e = ca::launch_rmsnorm(x, x_stride, residual, r_stride, sum_out, s_stride, w, y, y_stride, rows, n, eps,
+                                      static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm launch");
+    return ok();
+}
+
+int ca_swiglu(const uint16_t* gate, int64_t g_stride, const uint16_t* up, int64_t u_stride, uint16_t* y,
+              int64_t y_stride, int64_t rows, int32_t n, void* stream) {
+    if (gate == nullptr || up == nullptr || y == nullptr) return fail(CA_ERR_INVALID, "gate, up and y are required");
+    if (!aligned16(gate) || !aligned16(up) || !aligned16(y))
+        return fail(CA_ERR_INVALID, "gate, up and y must be 16-byte aligned");
+    if (n < 8 || n % 8 || g_stride % 8 || u_stride % 8 || y_stride % 8 || g_stride < n || u_stride < n || y_stride < n)
+        return fail(CA_ERR_INVALID, "n=%d must be a positive multiple of 8 and the row strides multiples of 8 >= n", n);
+    if (rows < 0 || rows * (n / 8) >= ((int64_t)1 << 38)) return fail(CA_ERR_LIMIT, "too many elements");
+    if (rows == 0) return ok();
+    hipError_t e = ca::launch_swiglu(gate, g_stride, up, u_stride, y, y_stride, rows, n, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "swiglu launch");
+    return ok();
+}

@@ -100,4 +100,13 @@ int attn_pick_splits(const Shape& s, const PastBlocks& pb, const int32_t* kv_len
 int64_t attn_workspace_bytes(const Shape& s, int num_splits);
 hipError_t launch_attn(const AttnArgs& a, hipStream_t stream);
 
+// model plumbing (ca_model.hip)
+hipError_t launch_rope(const SeqAddr& x, const SeqAddr& y, const float* cos, const float* sin, int B, int L, int H,
+                       hipStream_t stream);
+hipError_t launch_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* r, int64_t r_stride, uint16_t* s,
+                          int64_t s_stride, const uint16_t* w, uint16_t* y, int64_t y_stride, int64_t rows, int n,
+                          float eps, hipStream_t stream);
+hipError_t launch_swiglu(const uint16_t* g, int64_t g_stride, const uint16_t* u, int64_t u_stride, uint16_t* y,
+                         int64_t y_stride, int64_t rows, int n, hipStream_t stream);
+
 }  // namespace ca

@@ -395,3 +395,62 @@ def attn_decode(q: torch.Tensor, k: KV, v: KV, kv_len: Sequence[int], scale: flo
                                     ka, float(scale), ctypes.byref(ol), _ptr(lse), int(num_splits),
                                     _ptr(workspace), int(need), _stream()))
     return (out, lse) if with_lse else out
+
+
+# ----------------------------------------------------------------------------- model plumbing
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16(x * cos + rotate_half(x) * sin) for x [B, L, H, 128] bf16 and fp32 cos/sin [L, 128];
+    bit-identical to apply_rotary_pos_emb evaluated in fp32."""
+    B, L, H, _ = x.shape
+    xl = seq_layout(x, "x")
+    for name, t in (("cos", cos), ("sin", sin)):
+        _need_cuda(name, t, torch.float32)
+        if t.shape != (L, HEAD_DIM) or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous fp32 [{L}, {HEAD_DIM}]")
+    if out is None:
+        out = torch.empty((B, L, H, HEAD_DIM), dtype=torch.bfloat16, device=x.device)
+    yl = seq_layout(out, "out")
+    check(_hip.lib().ca_rope_apply(ctypes.byref(xl), ctypes.byref(yl), B, L, H, cos.data_ptr(), sin.data_ptr(),
+                                   _stream()))
+    return out
+
+
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float, residual: Optional[torch.Tensor] = None):
+    """bf16(w * bf16(x * rsqrt(mean(x^2) + eps))) over the last dim of a bf16 tensor.  With
+    ``residual`` the norm is taken of s = bf16(x + residual) and (s, y) is returned."""
+    _need_cuda("x", x, torch.bfloat16)
+    _need_cuda("weight", weight, torch.bfloat16)
+    n = x.shape[-1]
+    if weight.shape != (n,) or not weight.is_contiguous() or x.stride(-1) != 1:
+        raise ValueError("x needs a contiguous last dim and weight [n]")
+    x2 = x.reshape(-1, n)
+    out = torch.empty((x2.shape[0], n), dtype=torch.bfloat16, device=x.device)
+    r_ptr = s_ptr = 0
+    r2 = s2 = None
+    if residual is not None:
+        _need_cuda("residual", residual, torch.bfloat16)
+        if residual.shape != x.shape or residual.stride(-1) != 1:
+            raise ValueError("residual must match x's shape with a contiguous last dim")
+        r2 = residual.reshape(-1, n)
+        s2 = torch.empty_like(out)
+        r_ptr, s_ptr = r2.data_ptr(), s2.data_ptr()
+    check(_hip.lib().ca_rmsnorm(x2.data_ptr(), x2.stride(0), r_ptr, r2.stride(0) if r2 is not None else 0, s_ptr,
+                                s2.stride(0) if s2 is not None else 0, weight.data_ptr(), out.data_ptr(),
+                                out.stride(0), x2.shape[0], n, float(eps), _stream()))
+    if residual is None:
+        return out.view(x.shape)
+    return s2.view(x.shape), out.view(x.shape)
+
+
+def swiglu(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """bf16(bf16(silu(gate)) * up) for bf16 tensors of one shape."""
+    _need_cuda("gate", gate, torch.bfloat16)
+    _need_cuda("up", up, torch.bfloat16)
+    if gate.shape != up.shape or gate.stride(-1) != 1 or up.stride(-1) != 1:
+        raise ValueError("gate and up must share a shape with contiguous last dims")
+    n = gate.shape[-1]
+    g2, u2 = gate.reshape(-1, n), up.reshape(-1, n)
+    out = torch.empty((g2.shape[0], n), dtype=torch.bfloat16, device=gate.device)
+    check(_hip.lib().ca_swiglu(g2.data_ptr(), g2.stride(0), u2.data_ptr(), u2.stride(0), out.data_ptr(), out.stride(0),
+                               g2.shape[0], n, _stream()))
+    return out.view(gate.shape)

@@ -17,7 +17,6 @@ from __future__ import annotations
 from typing import List, Optional, Tuple, Type
 
 import torch
-import torch.nn.functional as F
 from torch import nn
 
 from ... import ops
@@ -33,10 +32,12 @@ class LlamaRMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=dtype))
         self.eps = eps
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
-        # statistics in fp32, as transformers' LlamaRMSNorm
-        y = F.rms_norm(x.float(), (x.shape[-1],), eps=self.eps)
-        return self.weight * y.to(x.dtype)
+    def forward(self, x: torch.Tensor, residual: Optional[torch.Tensor] = None):
+        """transformers' LlamaRMSNorm formula (fp32 statistics, bf16 normalised value times
+        the weight) in one HIP kernel.  With ``residual`` the norm is taken of
+        bf16(x + residual) and (sum, normed) is returned: the decoder's residual add fused
+        into the norm that follows it."""
+        return ops.rmsnorm(x, self.weight, self.eps, residual=residual)
 
 
 class LlamaMLP(nn.Module):
@@ -48,7 +49,8 @@ class LlamaMLP(nn.Module):
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, **kw)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        # bf16(silu(gate)) * up in one HIP kernel (F.silu(gate) * up, rounded alike)
+        return self.down_proj(ops.swiglu(self.gate_proj(x), self.up_proj(x)))
 
 
 class LlamaRotaryEmbedding(nn.Module):
@@ -91,6 +93,13 @@ def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, si
     return (qf * c + rotate_half(qf) * s).to(q.dtype), (kf * c + rotate_half(kf) * s).to(k.dtype)
 
 
+def rope_qk(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
+            ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """apply_rotary_pos_emb through the HIP rotary kernel (bit-identical results)."""
+    cos, sin = cos.float().contiguous(), sin.float().contiguous()
+    return ops.rope(q, cos, sin), ops.rope(k, cos, sin)
+
+
 def dense_decode_forward(attn: nn.Module, hidden_states: torch.Tensor, position_embeddings, cache: PagedKVCache):
     """Decode step(s) of a compactattn attention module: up to 64 new tokens per request
     attend densely to the whole cache (the reference routes q_len == 1 to dense attention,
@@ -103,7 +112,7 @@ def dense_decode_forward(attn: nn.Module, hidden_states: torch.Tensor, position_
     k = attn.k_proj(hidden_states).view(B, L, attn.num_key_value_heads, attn.head_dim)
     v = attn.v_proj(hidden_states).view(B, L, attn.num_key_value_heads, attn.head_dim)
     cos, sin = position_embeddings
-    query_states, key_states = apply_rotary_pos_emb(q, k, cos, sin)
+    query_states, key_states = rope_qk(q, k, cos, sin)
     cache.append_tokens(key_states, v)
     K, V = cache.layouts()
     out = ops.attn_decode(query_states.contiguous(), K, V, [cache.length] * B, attn.scaling, cache.cap,
@@ -148,15 +157,20 @@ class CompactAttnLlamaDecoderLayer(nn.Module):
         self.post_attention_layernorm = LlamaRMSNorm(config.hidden_size, config.rms_norm_eps, device=device)
 
     def forward(self, hidden_states: torch.Tensor, position_embeddings, block_position_embeddings,
-                past_key_value: ChunkedPrefillCache) -> torch.Tensor:
-        residual = hidden_states
-        h = self.input_layernorm(hidden_states)
+                past_key_value: ChunkedPrefillCache, residual: Optional[torch.Tensor] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """The layer's input is residual + hidden_states (hidden_states alone when residual
+        is None); returns (mlp_out, residual) whose sum is the layer's output.  Each residual
+        add is fused into the norm that follows it, with the same bf16 rounding as the
+        unfused ``residual + h``."""
+        if residual is None:
+            residual, h = hidden_states, self.input_layernorm(hidden_states)
+        else:
+            residual, h = self.input_layernorm(hidden_states, residual)
         h = self.self_attn(h, position_embeddings, None, past_key_value=past_key_value,
                            block_position_embeddings=block_position_embeddings)[0]
-        hidden_states = residual + h
-        residual = hidden_states
-        h = self.mlp(self.post_attention_layernorm(hidden_states))
-        return residual + h
+        residual, h = self.post_attention_layernorm(h, residual)
+        return self.mlp(h), residual
 
 
 class CompactAttnLlamaModel(nn.Module):
@@ -174,9 +188,10 @@ class CompactAttnLlamaModel(nn.Module):
         h = self.embed_tokens(input_ids)
         pos = self.rotary_emb.tokens(start, input_ids.shape[1])
         blk = self.rotary_emb.blocks()
+        residual = None
         for layer in self.layers:
-            h = layer(h, pos, blk, past_key_values)
-        return self.norm(h)
+            h, residual = layer(h, pos, blk, past_key_values, residual)
+        return self.norm(h, residual)[1]
 
 
 class CompactAttnLlamaForCausalLM(nn.Module):

@@ -32,7 +32,7 @@ from ... import ops
 from ...modules._core import COMPACTATTN_VERSION
 from ..attn_gate import AttnGate
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
-from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, apply_rotary_pos_emb,
+from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, rope_qk,
                                      dense_decode_forward, is_decode_step)
 
 BLOCK = 64
@@ -122,7 +122,7 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         k = self.k_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
         v = self.v_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
         cos, sin = position_embeddings
-        query_states, key_states = apply_rotary_pos_emb(q, k, cos, sin)
+        query_states, key_states = rope_qk(q, k, cos, sin)
 
         cache = past_key_value.layer(self.layer_idx)
         past = cache.append(key_states, v.contiguous())

@@ -254,6 +254,28 @@ int ca_attn_decode(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layo
 int64_t ca_attn_decode_workspace_size(const ca_dims* dims, const int32_t* kv_len_host,
                                       int32_t num_splits);
 
+/*
+ * Model plumbing.  Fused element-wise kernels of the Llama integration; they have no
+ * counterpart in _C_compactattn and replace chains of PyTorch element-wise kernels around
+ * the compactattn layers (bf16 in and out, fp32 math).
+ *
+ * ca_rope_apply: y = bf16(x * cos + rotate_half(x) * sin) for x, y [B, len, heads, 128]
+ * (seq layouts that must not overlap), cos/sin fp32 [len, 128] contiguous (the rows of the
+ * len positions); bit-identical to apply_rotary_pos_emb evaluated in fp32.
+ * ca_rmsnorm: y = bf16(w * bf16(s * rsqrt(mean(s^2) + eps))) per row of n (multiple of 8),
+ * s = x; with a residual (residual and sum_out both non-NULL) s = bf16(x + residual) is
+ * written to sum_out first (the decoder's residual add fused into the following norm;
+ * sum_out may alias x or residual, y must not overlap them).
+ * ca_swiglu: y = bf16(bf16(silu(gate)) * up) per row of n (multiple of 8).
+ */
+int ca_rope_apply(const ca_seq_layout* x, const ca_seq_layout* y, int32_t batch, int32_t len, int32_t heads,
+                  const float* cos, const float* sin, void* stream);
+int ca_rmsnorm(const uint16_t* x, int64_t x_stride, const uint16_t* residual, int64_t r_stride, uint16_t* sum_out,
+               int64_t s_stride, const uint16_t* w, uint16_t* y, int64_t y_stride, int64_t rows, int32_t n, float eps,
+               void* stream);
+int ca_swiglu(const uint16_t* gate, int64_t g_stride, const uint16_t* up, int64_t u_stride, uint16_t* y,
+              int64_t y_stride, int64_t rows, int32_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -224,3 +224,34 @@ def test_ops_reject_cpu_tensors():
     q = torch.zeros((1, 128, 8, 128), dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU tensor"):
         ops.pool_query(q, [0], 2)
+
+
+def test_model_plumbing_validation():
+    lib = _hip.lib()
+    x = _seq(FAKE, 64 * 8 * 128, 8 * 128, 128)
+    assert lib.ca_rope_apply(ctypes.byref(x), ctypes.byref(x), 0, 64, 8, FAKE, FAKE, None) == _hip.CA_ERR_INVALID
+    assert lib.ca_rope_apply(ctypes.byref(x), ctypes.byref(x), 1, 64, 8, None, FAKE, None) == _hip.CA_ERR_INVALID
+    assert "cos" in _hip.last_error()
+    rms = lambda n, rows=4, res=0, s=0, eps=1e-5: lib.ca_rmsnorm(FAKE, n, res, n, s, n, FAKE, FAKE, n,  # noqa: E731
+                                                                 rows, n, eps, None)
+    assert rms(12) == _hip.CA_ERR_INVALID and "n=12" in _hip.last_error()
+    assert rms(64, res=FAKE) == _hip.CA_ERR_INVALID and "together" in _hip.last_error()
+    assert rms(64, eps=-1.0) == _hip.CA_ERR_INVALID
+    assert rms(64, rows=1 << 31) == _hip.CA_ERR_LIMIT
+    assert rms(64, rows=0, res=FAKE, s=FAKE) == _hip.CA_OK  # nothing to launch
+    assert lib.ca_rmsnorm(FAKE, 64, 0, 0, 0, 0, FAKE + 2, FAKE, 64, 4, 64, 1e-5, None) == _hip.CA_ERR_INVALID
+    swi = lambda n, gs, rows=4: lib.ca_swiglu(FAKE, gs, FAKE, n, FAKE, n, rows, n, None)  # noqa: E731
+    assert swi(4, 4) == _hip.CA_ERR_INVALID
+    assert swi(64, 32) == _hip.CA_ERR_INVALID and "strides" in _hip.last_error()
+    assert swi(64, 128, rows=0) == _hip.CA_OK
+    assert lib.ca_swiglu(None, 64, FAKE, 64, FAKE, 64, 4, 64, None) == _hip.CA_ERR_INVALID
+
+
+def test_model_plumbing_python_errors():
+    x = torch.zeros((2, 64), dtype=torch.bfloat16)
+    with pytest.raises((ValueError, RuntimeError)):
+        ops.rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), 1e-5)
+    with pytest.raises((ValueError, RuntimeError)):
+        ops.swiglu(x, x)
+    with pytest.raises((ValueError, RuntimeError)):
+        ops.rope(torch.zeros((1, 64, 2, 128), dtype=torch.bfloat16), torch.zeros(64, 128), torch.zeros(64, 128))
