@@ -173,16 +173,49 @@ def main() -> int:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / reps * 1e3  # us
 
+    # ---- device time per call: the calls captured in one HIP graph and replayed, so the
+    # host's launch cost (Python + ctypes, several us per call) is not counted ----
+    def graph_timed(fn, reps=10, replays=5):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(reps):
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / (reps * replays) * 1e3  # us
+
     qhat = ops.pool_query(q, P, cap)
     rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, HKV, cap)
-    stage_us = {
-        "cache_fill": timed(lambda: ops.cache_fill(k_new, v_new, K, V, P, cap, kmean)),
-        "pool_query": timed(lambda: ops.pool_query(q, P, cap)),
-        "score_select": timed(lambda: ops.score_select(qhat, kmean, scale, rule, P, HKV, cap)),
-        "union_compact": timed(lambda: ops.union_compact(rowmask, P, HKV, cap)),
-        "attention": timed(lambda: ops.attn_fwd(q, K, V, table, counts, P, scale, cap, HKV, out=out,
-                                                num_splits=splits, workspace=ws)),
+    stage_fns = {
+        "cache_fill": lambda: ops.cache_fill(k_new, v_new, K, V, P, cap, kmean),
+        "pool_query": lambda: ops.pool_query(q, P, cap),
+        "score_select": lambda: ops.score_select(qhat, kmean, scale, rule, P, HKV, cap),
+        "union_compact": lambda: ops.union_compact(rowmask, P, HKV, cap),
+        "attention": lambda: ops.attn_fwd(q, K, V, table, counts, P, scale, cap, HKV, out=out, num_splits=splits,
+                                          workspace=ws),
     }
+    # eager per-call times (launch stream events; the small stages are bound by the host's
+    # launch rate here) and device times from graph replays
+    stage_us_eager = {k: timed(fn) for k, fn in stage_fns.items()}
+    stage_us = {k: graph_timed(fn) for k, fn in stage_fns.items()}
+    stage_us["attention"] = stage_us_eager["attention"]  # one long launch: host cost hidden
+    path_us_graph = graph_timed(step, reps=5, replays=4)
+    attn_us_graph = graph_timed(stage_fns["attention"], reps=5, replays=4)
+    progress(f"graph-replayed path: {path_us_graph:.1f} us per chunk")
 
     def attn_flops(cnts):
         per_row = [4.0 * 128 * G * (LQ * (int(c) - QB) * 64 + LQ * (LQ + 1) / 2) for c in cnts.tolist()]
@@ -251,7 +284,10 @@ def main() -> int:
         "speedup_vs_dense": round(dense_us / us_per_chunk, 3),
         "attn_speedup_vs_dense": round(dense_us / stage_us["attention"], 3),
         "dense_tflops": round(dense_tflops, 1),
+        "path_us_graph": round(path_us_graph, 2),
+        "attn_us_graph": round(attn_us_graph, 2),
         "stage_us": {k: round(v, 2) for k, v in stage_us.items()},
+        "stage_us_eager": {k: round(v, 2) for k, v in stage_us_eager.items()},
         "stage_hbm_frac": hbm_frac,
         "sweep": sweep,
         "roofline": {
