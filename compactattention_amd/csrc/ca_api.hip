@@ -448,8 +448,10 @@ int ca_rope_apply(const ca_seq_layout* x, const ca_seq_layout* y, int32_t batch,
     if ((rc = check_seq(x, "x", &xa)) != CA_OK) return rc;
     if ((rc = check_seq(y, "y", &ya)) != CA_OK) return rc;
     if (batch < 1 || len < 1 || heads < 1) return fail(CA_ERR_INVALID, "batch, len and heads must be positive");
-    if ((int64_t)batch * len * heads * 16 >= ((int64_t)1 << 40)) return fail(CA_ERR_LIMIT, "too many rows");
+    if ((int64_t)batch * len >= ((int64_t)1 << 31) || heads > 65535)
+        return fail(CA_ERR_LIMIT, "batch * len must be below 2^31 and heads at most 65535");
     if (cos == nullptr || sin == nullptr) return fail(CA_ERR_INVALID, "cos and sin are required");
+    if (!aligned16(cos) || !aligned16(sin)) return fail(CA_ERR_INVALID, "cos and sin must be 16-byte aligned");
     hipError_t e = ca::launch_rope(xa, ya, cos, sin, batch, len, heads, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "rope launch");
     return ok();

@@ -7,8 +7,8 @@
 //  - rotary: out = bf16(q * cos + rotate_half(q) * sin), every product and the sum rounded
 //    to fp32 separately (-ffp-contract=off) -- the same operations, in the same order, as
 //    apply_rotary_pos_emb in fp32 (modeling_llama_common.py), so the result is bit-identical;
-//  - RMSNorm: y = bf16(w * bf16(x * rsqrt(mean(x^2) + eps))), the transformers formula; the
-//    mean's summation order is this kernel's own.  The residual form first adds the
+//  - RMSNorm: y = bf16(w * bf16(x * (1 / sqrt(mean(x^2) + eps)))), the transformers formula;
+//    the mean's summation order is this kernel's own.  The residual form first adds the
 //    residual in bf16 (x + r rounded once, as the decoder's residual + h) and normalises
 //    that sum, returning both;
 //  - SwiGLU: out = bf16(bf16(silu(g)) * u), silu in fp32.
@@ -22,7 +22,9 @@ namespace {
 typedef uint16_t u16x8_t __attribute__((ext_vector_type(8)));
 
 // One thread per 8 elements of a head row: lanes 0-7 hold d = 0..63 (their rotate partner
-// d + 64 is read alongside), lanes 8-15 hold d = 64..127.
+// d + 64 is read alongside), lanes 8-15 hold d = 64..127.  blockIdx.x is the token row
+// (b * L + t), so a workgroup covers 16 heads of one token and the thread's head and chunk
+// come from its index without divisions.
 struct RopeParams {
     const uint16_t* x;
     int64_t xsb, xst, xsh;
@@ -34,31 +36,32 @@ struct RopeParams {
 };
 
 __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t total = (int64_t)p.B * p.L * p.H * 16;
-    if (gid >= total) return;
-    const int c = static_cast<int>(gid & 15);  // 8-element chunk of the 128-wide row
-    int64_t r = gid >> 4;
-    const int h = static_cast<int>(r % p.H);
-    r /= p.H;
-    const int t = static_cast<int>(r % p.L);
-    const int b = static_cast<int>(r / p.L);
+    const int bt = blockIdx.x;
+    const int idx = blockIdx.y * 256 + threadIdx.x;
+    const int h = idx >> 4;
+    if (h >= p.H) return;
+    const int c = idx & 15;  // 8-element chunk of the 128-wide row
+    const int b = bt / p.L;
+    const int t = bt - b * p.L;
     const uint16_t* xr = p.x + b * p.xsb + (int64_t)t * p.xst + (int64_t)h * p.xsh;
     uint16_t* yr = p.y + b * p.ysb + (int64_t)t * p.yst + (int64_t)h * p.ysh;
     const int d0 = 8 * c;
     const int dp = d0 < 64 ? d0 + 64 : d0 - 64;  // rotate_half partner
     const u16x8_t xv = *reinterpret_cast<const u16x8_t*>(xr + d0);
     const u16x8_t pv = *reinterpret_cast<const u16x8_t*>(xr + dp);
-    const float* cr = p.cos + (int64_t)t * 128 + d0;
-    const float* sr = p.sin + (int64_t)t * 128 + d0;
+    const float4* cr = reinterpret_cast<const float4*>(p.cos + (int64_t)t * 128 + d0);
+    const float4* sr = reinterpret_cast<const float4*>(p.sin + (int64_t)t * 128 + d0);
+    const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+    const float cv[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+    const float sv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
     u16x8_t out;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const float xi = bf16_to_f32(xv[i]);
         const float pi = bf16_to_f32(pv[i]);
         const float rot = d0 < 64 ? -pi : pi;
-        const float a = xi * cr[i];
-        const float bb = rot * sr[i];
+        const float a = xi * cv[i];
+        const float bb = rot * sv[i];
         out[i] = f32_to_bf16(a + bb);
     }
     *reinterpret_cast<u16x8_t*>(yr + d0) = out;
@@ -69,7 +72,7 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeParams p) {
 // is deterministic).  n must be a multiple of 8 (checked on the host).  With a residual the
 // row is first s = bf16(x + r), written to s_out (the residual stream of the decoder layer),
 // and the norm is taken of s; a thread re-reads only the elements it wrote itself, so s_out
-// may alias x or r.
+// may alias x or r.  Up to kRmsKeep chunks per thread stay in registers between the passes.
 struct RmsParams {
     const uint16_t* x;
     int64_t x_stride;
@@ -84,6 +87,8 @@ struct RmsParams {
     float eps;
 };
 
+constexpr int kRmsKeep = 4;  // chunks per thread held in registers: rows up to 8192 elements
+
 __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsParams p) {
     __shared__ float part[4];
     const int64_t row = blockIdx.x;
@@ -91,8 +96,8 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsParams p) {
     uint16_t* yr = p.y + row * p.y_stride;
     const bool add = p.r != nullptr;
     const uint16_t* src = add ? p.s + row * p.s_stride : xr;
-    float ss = 0.0f;
-    for (int i = threadIdx.x * 8; i < p.n; i += 256 * 8) {
+    // pass 1 over the thread's chunk i = 8 (t + 256 k): the (summed) row value, its square
+    auto load = [&](int i, float& ss) {
         u16x8_t v = *reinterpret_cast<const u16x8_t*>(xr + i);
         if (add) {
             const u16x8_t rv = *reinterpret_cast<const u16x8_t*>(p.r + row * p.r_stride + i);
@@ -105,15 +110,23 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsParams p) {
             const float f = bf16_to_f32(v[j]);
             ss = __builtin_fmaf(f, f, ss);
         }
+        return v;
+    };
+    float ss = 0.0f;
+    u16x8_t keep[kRmsKeep];
+#pragma unroll
+    for (int k = 0; k < kRmsKeep; ++k) {
+        const int i = threadIdx.x * 8 + k * 2048;
+        if (i < p.n) keep[k] = load(i, ss);
     }
+    for (int i = threadIdx.x * 8 + kRmsKeep * 2048; i < p.n; i += 2048) load(i, ss);
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);
     if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
     __syncthreads();
     const float total = (part[0] + part[1]) + (part[2] + part[3]);
     const float rstd = 1.0f / __builtin_sqrtf(total / static_cast<float>(p.n) + p.eps);
-    for (int i = threadIdx.x * 8; i < p.n; i += 256 * 8) {
-        const u16x8_t v = *reinterpret_cast<const u16x8_t*>(src + i);
+    auto store = [&](int i, const u16x8_t& v) {
         const u16x8_t wv = *reinterpret_cast<const u16x8_t*>(p.w + i);
         u16x8_t o;
 #pragma unroll
@@ -122,7 +135,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(RmsParams p) {
             o[j] = f32_to_bf16(bf16_to_f32(wv[j]) * yn);
         }
         *reinterpret_cast<u16x8_t*>(yr + i) = o;
+    };
+#pragma unroll
+    for (int k = 0; k < kRmsKeep; ++k) {
+        const int i = threadIdx.x * 8 + k * 2048;
+        if (i < p.n) store(i, keep[k]);
     }
+    for (int i = threadIdx.x * 8 + kRmsKeep * 2048; i < p.n; i += 2048)
+        store(i, *reinterpret_cast<const u16x8_t*>(src + i));
 }
 
 struct SwigluParams {
@@ -172,8 +192,8 @@ hipError_t launch_rope(const SeqAddr& x, const SeqAddr& y, const float* cos, con
     p.B = B;
     p.L = L;
     p.H = H;
-    const int64_t total = (int64_t)B * L * H * 16;
-    hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL(rope_kernel, dim3(static_cast<unsigned>((int64_t)B * L), static_cast<unsigned>((H * 16 + 255) / 256)),
+                       dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 

@@ -198,6 +198,7 @@ def load_llama_attention_replacement_model(
         for name in ("q_proj", "k_proj", "v_proj", "o_proj"):
             setattr(impl, name, getattr(src, name))
         impl.to(device=dev)  # the gate stays fp32, the projections keep the model's dtype
+        impl.qkv.refuse()  # one GEMM for the stock q/k/v projections (weights re-seated, not copied)
         _adapt_to_transformers(impl, block_rope)
         layer.self_attn = impl
     model.eval()

@@ -14,9 +14,10 @@ take the row of each block's first token (modeling_llama_seerattn.py:896-897).
 """
 from __future__ import annotations
 
-from typing import List, Optional, Tuple, Type
+from typing import List, Optional, Sequence, Tuple, Type
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from ... import ops
@@ -24,6 +25,46 @@ from ...kv_cache import PagedKVCache
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 
 BLOCK = 64
+
+
+class FusedProjections:
+    """One GEMM for several bias-free nn.Linear modules of the owner that read the same
+    input (q/k/v, gate/up).  Their weights are re-seated as row blocks (views) of one
+    contiguous [sum(out_features), in_features] store, so the modules, their parameters and
+    their state_dict keys stay as they are and nothing is duplicated.  The modules are looked
+    up by name on every call: if one was replaced, re-created or moved (Module.to), the store
+    no longer backs it and the modules are called one by one; ``refuse()`` re-seats them."""
+
+    def __init__(self, owner: nn.Module, names: Sequence[str]):
+        self.owner = owner
+        self.names = tuple(names)
+        self.refuse()
+
+    def refuse(self) -> None:
+        mods = [getattr(self.owner, n) for n in self.names]
+        self.sizes = [m.out_features for m in mods]
+        self.store = torch.cat([m.weight.detach() for m in mods], 0)
+        off = 0
+        for m, n in zip(mods, self.sizes):
+            m.weight = nn.Parameter(self.store[off:off + n], requires_grad=m.weight.requires_grad)
+            off += n
+
+    def intact(self) -> bool:
+        row_bytes = self.store.shape[1] * self.store.element_size()
+        off = 0
+        for name, n in zip(self.names, self.sizes):
+            m = getattr(self.owner, name)
+            w = m.weight
+            if (m.bias is not None or w.shape != (n, self.store.shape[1]) or w.dtype != self.store.dtype
+                    or w.data_ptr() != self.store.data_ptr() + off * row_bytes):
+                return False
+            off += n
+        return True
+
+    def __call__(self, x: torch.Tensor) -> Tuple[torch.Tensor, ...]:
+        if self.intact():
+            return F.linear(x, self.store).split(self.sizes, dim=-1)
+        return tuple(getattr(self.owner, n)(x) for n in self.names)
 
 
 class LlamaRMSNorm(nn.Module):
@@ -47,10 +88,13 @@ class LlamaMLP(nn.Module):
         self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, **kw)
         self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, **kw)
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, **kw)
+        self.gate_up = FusedProjections(self, ("gate_proj", "up_proj"))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        # bf16(silu(gate)) * up in one HIP kernel (F.silu(gate) * up, rounded alike)
-        return self.down_proj(ops.swiglu(self.gate_proj(x), self.up_proj(x)))
+        # one GEMM for gate and up; bf16(silu(gate)) * up in one HIP kernel (F.silu(gate) * up,
+        # rounded alike)
+        gate, up = self.gate_up(x)
+        return self.down_proj(ops.swiglu(gate, up))
 
 
 class LlamaRotaryEmbedding(nn.Module):
@@ -93,6 +137,15 @@ def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, si
     return (qf * c + rotate_half(qf) * s).to(q.dtype), (kf * c + rotate_half(kf) * s).to(k.dtype)
 
 
+def project_qkv(attn: nn.Module, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """q [B, L, Hq, D], k and v [B, L, Hkv, D] (strided views of one GEMM's output when the
+    module's projections are fused)."""
+    B, L, _ = hidden_states.shape
+    q, k, v = attn.qkv(hidden_states)
+    return (q.view(B, L, attn.num_heads, attn.head_dim), k.view(B, L, attn.num_key_value_heads, attn.head_dim),
+            v.view(B, L, attn.num_key_value_heads, attn.head_dim))
+
+
 def rope_qk(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor
             ) -> Tuple[torch.Tensor, torch.Tensor]:
     """apply_rotary_pos_emb through the HIP rotary kernel (bit-identical results)."""
@@ -108,9 +161,7 @@ def dense_decode_forward(attn: nn.Module, hidden_states: torch.Tensor, position_
     B, L, _ = hidden_states.shape
     if L > BLOCK:
         raise ValueError(f"decode steps take at most {BLOCK} tokens per call (got {L})")
-    q = attn.q_proj(hidden_states).view(B, L, attn.num_heads, attn.head_dim)
-    k = attn.k_proj(hidden_states).view(B, L, attn.num_key_value_heads, attn.head_dim)
-    v = attn.v_proj(hidden_states).view(B, L, attn.num_key_value_heads, attn.head_dim)
+    q, k, v = project_qkv(attn, hidden_states)
     cos, sin = position_embeddings
     query_states, key_states = rope_qk(q, k, cos, sin)
     cache.append_tokens(key_states, v)

@@ -25,8 +25,8 @@ from ... import ops
 from ...modules._core import COMPACTATTN_VERSION
 from ...modules.flashprefill_prefill import flashprefill_rule
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
-from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, rope_qk,
-                                     dense_decode_forward, is_decode_step)
+from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
+                                     dense_decode_forward, is_decode_step, project_qkv, rope_qk)
 
 BLOCK = 64
 
@@ -46,6 +46,7 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
         self.k_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
+        self.qkv = FusedProjections(self, ("q_proj", "k_proj", "v_proj"))
         self.compactattn_version = COMPACTATTN_VERSION
         self.compactattn_debug = False
         self._compactattn_last_stats = None
@@ -71,9 +72,7 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
         B, L, _ = hidden_states.shape
         if L % BLOCK:
             raise ValueError("chunk lengths must be multiples of 64 tokens")
-        q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim)
-        k = self.k_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
-        v = self.v_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
+        q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
         query_states, key_states = rope_qk(q, k, cos, sin)
 

@@ -32,8 +32,8 @@ from ... import ops
 from ...modules._core import COMPACTATTN_VERSION
 from ..attn_gate import AttnGate
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
-from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, rope_qk,
-                                     dense_decode_forward, is_decode_step)
+from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
+                                     dense_decode_forward, is_decode_step, project_qkv, rope_qk)
 
 BLOCK = 64
 
@@ -53,6 +53,7 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         self.k_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
+        self.qkv = FusedProjections(self, ("q_proj", "k_proj", "v_proj"))
         self.attn_gate = AttnGate(config.seerattn_gate_block_size, self.head_dim, config.seerattn_gate_hidden_size,
                                   self.num_key_value_heads, self.num_heads,
                                   force_double=config.seerattn_gate_force_double).to(device)
@@ -118,9 +119,7 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         B, L, _ = hidden_states.shape
         if L % BLOCK:
             raise ValueError("chunk lengths must be multiples of 64 tokens")
-        q = self.q_proj(hidden_states).view(B, L, self.num_heads, self.head_dim)
-        k = self.k_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
-        v = self.v_proj(hidden_states).view(B, L, self.num_key_value_heads, self.head_dim)
+        q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
         query_states, key_states = rope_qk(q, k, cos, sin)
 

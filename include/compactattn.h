@@ -260,8 +260,9 @@ int64_t ca_attn_decode_workspace_size(const ca_dims* dims, const int32_t* kv_len
  * the compactattn layers (bf16 in and out, fp32 math).
  *
  * ca_rope_apply: y = bf16(x * cos + rotate_half(x) * sin) for x, y [B, len, heads, 128]
- * (seq layouts that must not overlap), cos/sin fp32 [len, 128] contiguous (the rows of the
- * len positions); bit-identical to apply_rotary_pos_emb evaluated in fp32.
+ * (seq layouts that must not overlap; batch * len < 2^31), cos/sin fp32 [len, 128]
+ * contiguous and 16-byte aligned (the rows of the len positions); bit-identical to
+ * apply_rotary_pos_emb evaluated in fp32.
  * ca_rmsnorm: y = bf16(w * bf16(s * rsqrt(mean(s^2) + eps))) per row of n (multiple of 8),
  * s = x; with a residual (residual and sum_out both non-NULL) s = bf16(x + residual) is
  * written to sum_out first (the decoder's residual add fused into the following norm;

@@ -21,7 +21,7 @@ import oracle
 from compactattention_amd.chunked_prefill import run_chunked_prefill_once, synthetic_prompt
 from compactattention_amd.prefill_sparse.llama import (SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaConfig,
                                                        SeerAttnLlamaFlashPrefillCompactAttnForCausalLM)
-from compactattention_amd.prefill_sparse.llama.modeling_llama_common import apply_rotary_pos_emb
+from compactattention_amd.prefill_sparse.llama.modeling_llama_common import apply_rotary_pos_emb, project_qkv
 
 from .util import bits, f32
 
@@ -191,9 +191,7 @@ def _capture_layer_inputs(model, layer_idx):
 
 def _layer_qkv(attn, hidden, start, model):
     B, L, _ = hidden.shape
-    q = attn.q_proj(hidden).view(B, L, attn.num_heads, 128)
-    k = attn.k_proj(hidden).view(B, L, attn.num_key_value_heads, 128)
-    v = attn.v_proj(hidden).view(B, L, attn.num_key_value_heads, 128)
+    q, k, v = project_qkv(attn, hidden)  # the layer's own (fused) projection GEMM
     cos, sin = model.model.rotary_emb.tokens(start, L)
     qr, kr = apply_rotary_pos_emb(q, k, cos, sin)
     return q, k, v, qr, kr

@@ -98,3 +98,40 @@ def test_paged_cache_decode_append_rules():
     with pytest.raises(ValueError, match="capacity"):
         c.append_tokens(torch.zeros((1, 126, 2, 128), dtype=torch.bfloat16),
                         torch.zeros((1, 126, 2, 128), dtype=torch.bfloat16))
+
+
+def test_fused_projections_reseat_weights_and_fall_back():
+    from torch import nn
+
+    from compactattention_amd.prefill_sparse.llama.modeling_llama_common import FusedProjections
+
+    torch.manual_seed(0)
+    owner = nn.Module()
+    owner.a = nn.Linear(16, 8, bias=False)
+    owner.b = nn.Linear(16, 4, bias=False)
+    ref_w = [owner.a.weight.detach().clone(), owner.b.weight.detach().clone()]
+    fused = FusedProjections(owner, ("a", "b"))
+    # the parameters are row blocks of one store, values and state_dict keys unchanged
+    assert fused.intact()
+    assert owner.a.weight.data_ptr() == fused.store.data_ptr()
+    assert owner.b.weight.data_ptr() == fused.store.data_ptr() + 8 * 16 * 4
+    assert torch.equal(owner.a.weight, ref_w[0]) and torch.equal(owner.b.weight, ref_w[1])
+    assert sorted(owner.state_dict()) == ["a.weight", "b.weight"]
+    x = torch.randn(3, 5, 16)
+    ya, yb = fused(x)
+    assert ya.shape == (3, 5, 8) and yb.shape == (3, 5, 4)
+    assert torch.allclose(ya, x @ ref_w[0].T, atol=1e-5) and torch.allclose(yb, x @ ref_w[1].T, atol=1e-5)
+    # in-place updates (init, load_state_dict) write through the views
+    with torch.no_grad():
+        owner.b.weight.mul_(2.0)
+    assert torch.allclose(fused(x)[1], x @ (2 * ref_w[1]).T, atol=1e-5)
+    # a replaced module is no longer backed by the store: the modules run one by one
+    owner.b = nn.Linear(16, 4, bias=False)
+    assert not fused.intact()
+    assert torch.allclose(fused(x)[1], owner.b(x))
+    fused.refuse()
+    assert fused.intact() and torch.allclose(fused(x)[1], x @ owner.b.weight.T, atol=1e-5)
+    # a dtype change (Module.to) also falls back
+    owner.to(torch.float64)
+    assert not fused.intact()
+    assert fused(x.double())[0].dtype == torch.float64
