@@ -536,9 +536,22 @@ def model_prefill(tokens, chunk, layers, dev):
             keeps.append(float((st["counts"].float() - qb).mean().item()) / st["past_blocks"])
     for layer in model.model.layers:
         layer.self_attn.compactattn_debug = False
+    def attention_share():
+        """Seconds of the attention core (RoPE, cache append, selection, attention kernels)
+        summed over layers and chunks from timing events, and the prefill's wall time."""
+        spans = []
+        for layer in model.model.layers:
+            layer.self_attn.attention_timer = spans
+        _, wall = run_chunked_prefill_once(model, ids, chunk, cache)
+        for layer in model.model.layers:
+            layer.self_attn.attention_timer = None
+        return sum(a.elapsed_time(b) for a, b in spans) * 1e-3, wall
+
+    attn_s, attn_wall = attention_share()
     cfg.seerattn_chunked_prefill_force_dense = True
     _, dense_s = run_chunked_prefill_once(model, ids, chunk, cache)
     progress(f"model prefill: dense {dense_s:.2f} s")
+    dense_attn_s, dense_attn_wall = attention_share()
     linear_flops = 2.0 * tokens * sum(p.numel() for n, p in model.named_parameters()
                                       if n.startswith("model.layers.") and "proj" in n and "attn_gate" not in n)
     del model, cache
@@ -553,6 +566,9 @@ def model_prefill(tokens, chunk, layers, dev):
         "dense_tok_per_s": round(tokens / dense_s, 1),
         "dense_seconds": round(dense_s, 3),
         "speedup_vs_dense": round(dense_s / compact_s, 3),
+        "attention_share": round(attn_s / attn_wall, 4),
+        "attention_s": round(attn_s, 3),
+        "dense_attention_share": round(dense_attn_s / dense_attn_wall, 4),
         "keep_ratio_last_chunk": round(sum(keeps) / max(len(keeps), 1), 4),
         "linear_tflops_per_s": round(linear_flops / compact_s / 1e12, 1),
     }

@@ -14,6 +14,7 @@ take the row of each block's first token (modeling_llama_seerattn.py:896-897).
 """
 from __future__ import annotations
 
+from contextlib import contextmanager
 from typing import List, Optional, Sequence, Tuple, Type
 
 import torch
@@ -135,6 +136,21 @@ def apply_rotary_pos_emb(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, si
     s = sin[None, :, None, :]
     qf, kf = q.float(), k.float()
     return (qf * c + rotate_half(qf) * s).to(q.dtype), (kf * c + rotate_half(kf) * s).to(k.dtype)
+
+
+@contextmanager
+def event_span(sink: Optional[list]):
+    """Records a (start, end) pair of timing events on the current stream around the block
+    into ``sink`` when it is a list (no-op for None): the attention share of a model run."""
+    if sink is None:
+        yield
+        return
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    yield
+    end.record()
+    sink.append((start, end))
 
 
 def project_qkv(attn: nn.Module, hidden_states: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:

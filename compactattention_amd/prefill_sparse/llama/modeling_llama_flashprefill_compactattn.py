@@ -26,7 +26,7 @@ from ...modules._core import COMPACTATTN_VERSION
 from ...modules.flashprefill_prefill import flashprefill_rule
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
-                                     dense_decode_forward, is_decode_step, project_qkv, rope_qk)
+                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk)
 
 BLOCK = 64
 
@@ -47,6 +47,7 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
         self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
         self.qkv = FusedProjections(self, ("q_proj", "k_proj", "v_proj"))
+        self.attention_timer: Optional[list] = None  # a list collects timing events of the attention core
         self.compactattn_version = COMPACTATTN_VERSION
         self.compactattn_debug = False
         self._compactattn_last_stats = None
@@ -74,24 +75,25 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
             raise ValueError("chunk lengths must be multiples of 64 tokens")
         q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
-        query_states, key_states = rope_qk(q, k, cos, sin)
-
-        cache = past_key_value.layer(self.layer_idx)
-        past = cache.append(key_states, v.contiguous())  # pages + mean-K of the new blocks
-        P = [past] * B
-        dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
-        if dense:
-            table, counts = ops.dense_table(P, L, self.num_heads, self.num_key_value_heads, cache.cap,
-                                            query_states.device)
-        else:
-            rule = self._selection_rule()
-            qhat = ops.pool_query(query_states, P, cache.cap, num_kv_heads=self.num_key_value_heads)
-            rowmask, _ = ops.score_select(qhat, cache.kmean, 1.0 / math.sqrt(self.head_dim), rule, P,
-                                          self.num_key_value_heads, cache.cap)
-            table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap,
-                                                    last_n_block=rule.last_n_block)
-        K, V = cache.layouts()
-        out = ops.attn_fwd(query_states, K, V, table, counts, P, self.scaling, cache.cap, self.num_key_value_heads)
+        with event_span(self.attention_timer):
+            query_states, key_states = rope_qk(q, k, cos, sin)
+            cache = past_key_value.layer(self.layer_idx)
+            past = cache.append(key_states, v.contiguous())  # pages + mean-K of the new blocks
+            P = [past] * B
+            dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
+            if dense:
+                table, counts = ops.dense_table(P, L, self.num_heads, self.num_key_value_heads, cache.cap,
+                                                query_states.device)
+            else:
+                rule = self._selection_rule()
+                qhat = ops.pool_query(query_states, P, cache.cap, num_kv_heads=self.num_key_value_heads)
+                rowmask, _ = ops.score_select(qhat, cache.kmean, 1.0 / math.sqrt(self.head_dim), rule, P,
+                                              self.num_key_value_heads, cache.cap)
+                table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap,
+                                                        last_n_block=rule.last_n_block)
+            K, V = cache.layouts()
+            out = ops.attn_fwd(query_states, K, V, table, counts, P, self.scaling, cache.cap,
+                               self.num_key_value_heads)
         out = self.o_proj(out.reshape(B, L, -1))
         if self.compactattn_debug:
             self._compactattn_last_stats = {

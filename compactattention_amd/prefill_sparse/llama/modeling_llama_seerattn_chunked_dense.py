@@ -33,7 +33,7 @@ from ...modules._core import COMPACTATTN_VERSION
 from ..attn_gate import AttnGate
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
-                                     dense_decode_forward, is_decode_step, project_qkv, rope_qk)
+                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk)
 
 BLOCK = 64
 
@@ -54,6 +54,7 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         self.v_proj = nn.Linear(config.hidden_size, self.num_key_value_heads * self.head_dim, **kw)
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
         self.qkv = FusedProjections(self, ("q_proj", "k_proj", "v_proj"))
+        self.attention_timer: Optional[list] = None  # a list collects timing events of the attention core
         self.attn_gate = AttnGate(config.seerattn_gate_block_size, self.head_dim, config.seerattn_gate_hidden_size,
                                   self.num_key_value_heads, self.num_heads,
                                   force_double=config.seerattn_gate_force_double).to(device)
@@ -121,14 +122,14 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
             raise ValueError("chunk lengths must be multiples of 64 tokens")
         q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
-        query_states, key_states = rope_qk(q, k, cos, sin)
-
-        cache = past_key_value.layer(self.layer_idx)
-        past = cache.append(key_states, v.contiguous())
-        self._append_compactattn_chunked_gate_key_cache(k.contiguous(), cache, past, block_position_embeddings)
-        dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
-        out, table, counts = self._do_chunked_compactattn_attention(query_states, q.contiguous(), cache, past,
-                                                                   block_position_embeddings, dense)
+        with event_span(self.attention_timer):
+            query_states, key_states = rope_qk(q, k, cos, sin)
+            cache = past_key_value.layer(self.layer_idx)
+            past = cache.append(key_states, v.contiguous())
+            self._append_compactattn_chunked_gate_key_cache(k.contiguous(), cache, past, block_position_embeddings)
+            dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
+            out, table, counts = self._do_chunked_compactattn_attention(query_states, q.contiguous(), cache, past,
+                                                                       block_position_embeddings, dense)
         out = self.o_proj(out.reshape(B, L, -1))
         if self.compactattn_debug:
             self._compactattn_last_stats = {
