@@ -15,8 +15,7 @@ evaluated at position_ids[:, 0::64]).
 """
 from __future__ import annotations
 
-import math
-from typing import Optional, Tuple
+from typing import Optional
 
 import torch
 from torch import nn

@@ -13,7 +13,6 @@ import pytest
 import torch
 
 import oracle
-from compactattention_amd import ops
 from compactattention_amd.flashprefill_vendor import flash_prefill_compute_mean_k, flash_prefill_score_chunked_from_mean_k
 from compactattention_amd.kv_cache import PagedKVCache
 from compactattention_amd.modules.attention_forward_chunked_dense import (
