@@ -78,7 +78,7 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
         with event_span(self.attention_timer):
             query_states, key_states = rope_qk(q, k, cos, sin)
             cache = past_key_value.layer(self.layer_idx)
-            past = cache.append(key_states, v.contiguous())  # pages + mean-K of the new blocks
+            past = cache.append(key_states, v)  # pages + mean-K of the new blocks (v may be strided)
             P = [past] * B
             dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
             if dense:

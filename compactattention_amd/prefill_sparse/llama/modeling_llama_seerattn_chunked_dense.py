@@ -125,10 +125,10 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         with event_span(self.attention_timer):
             query_states, key_states = rope_qk(q, k, cos, sin)
             cache = past_key_value.layer(self.layer_idx)
-            past = cache.append(key_states, v.contiguous())
-            self._append_compactattn_chunked_gate_key_cache(k.contiguous(), cache, past, block_position_embeddings)
+            past = cache.append(key_states, v)  # v, k and q may be strided views of the fused GEMM
+            self._append_compactattn_chunked_gate_key_cache(k, cache, past, block_position_embeddings)
             dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
-            out, table, counts = self._do_chunked_compactattn_attention(query_states, q.contiguous(), cache, past,
+            out, table, counts = self._do_chunked_compactattn_attention(query_states, q, cache, past,
                                                                        block_position_embeddings, dense)
         out = self.o_proj(out.reshape(B, L, -1))
         if self.compactattn_debug:
