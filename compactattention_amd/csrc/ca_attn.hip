@@ -816,6 +816,13 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
         forced = static_cast<int>(slots / (double)units + 0.5);
         forced = min(forced, max(1, nkb_max / min_blocks));
         forced = max(1, min(forced, max_splits));
+        // Requests of one length whose row tiles already fill three quarters of the CUs run
+        // unsplit: the items stay balanced and the split partials and their merge are saved
+        // (config-3 chunks, 256 tiles: 21 us of merge per layer).  Ragged batches keep the
+        // split, which balances their long rows against the short ones.
+        bool same_len = true;
+        for (int b = 1; b < s.B; ++b) same_len = same_len && nkb[b] == nkb[0];
+        if (same_len && units * 4 >= 3 * 256) forced = 1;
     }
     plan->max = 1;
     plan->off[0] = 0;
