@@ -334,6 +334,30 @@ __device__ __forceinline__ int wave_kth_smallest_id(const int (&id)[S], const bo
     return T;
 }
 
+// The k-th largest key T over the nl (<= 64 S) candidates held S per lane, and the id cut
+// among the candidates equal to T: the (k - #{key > T})-th smallest such id.
+template <int S>
+__device__ __forceinline__ void select_candidates(const uint32_t* cand_key, const int* cand_id, int nl, int lane,
+                                                  int k, uint32_t& T, int& eq_cut) {
+    uint32_t x[S];
+    int id[S];
+    bool eq[S];
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        const int j = lane + 64 * i;
+        x[i] = j < nl ? cand_key[j] : 0u;
+        id[i] = j < nl ? cand_id[j] : 0;
+    }
+    T = wave_kth_largest<S>(x, k);
+    int gt = 0;
+#pragma unroll
+    for (int i = 0; i < S; ++i) {
+        gt += __popcll(__ballot(x[i] > T));
+        eq[i] = x[i] == T;
+    }
+    eq_cut = wave_kth_smallest_id<S>(id, eq, k - gt);
+}
+
 template <bool kCompute>
 __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p) {
     extern __shared__ float row[];  // [cap]
@@ -497,24 +521,11 @@ __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p)
             const int nl = cand_n;
             uint32_t T;
             int eq_cut;
-            if (nl <= kCandCap) {
-                uint32_t x[kCandSlots];
-                int id[kCandSlots];
-                bool eq[kCandSlots];
-#pragma unroll
-                for (int i = 0; i < kCandSlots; ++i) {
-                    const int j = lane + 64 * i;
-                    x[i] = j < nl ? cand_key[j] : 0u;
-                    id[i] = j < nl ? cand_id[j] : 0;
-                }
-                T = wave_kth_largest<kCandSlots>(x, k);
-                int gt = 0;
-#pragma unroll
-                for (int i = 0; i < kCandSlots; ++i) {
-                    gt += __popcll(__ballot(x[i] > T));
-                    eq[i] = x[i] == T;
-                }
-                eq_cut = wave_kth_smallest_id<kCandSlots>(id, eq, k - gt);
+            if (nl <= 64) {
+                // the usual case: one candidate per lane
+                select_candidates<1>(cand_key, cand_id, nl, lane, k, T, eq_cut);
+            } else if (nl <= kCandCap) {
+                select_candidates<kCandSlots>(cand_key, cand_id, nl, lane, k, T, eq_cut);
             } else {
                 T = 0;
                 for (int bit = 31; bit >= 0; --bit) {
