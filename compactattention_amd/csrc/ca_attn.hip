@@ -787,8 +787,9 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
     // same number of blocks as everyone else's (total work / slots); attn_fwd_kernel uses
     // one split count for all requests (below).  Both keep a minimum number of blocks per
     // split and at most the entry point's maximum of splits.
-    //  - indexed prefill (attn_fwd_kernel): about two rounds of workgroups (2 x 256 slots),
-    //    at least ~16 blocks per split, at most 16 splits;
+    //  - indexed prefill (attn_fwd_kernel): about one round of workgroups (256 slots) for
+    //    requests of one length, two (512) for ragged batches, at least ~16 blocks per
+    //    split, at most 16 splits;
     //  - dense decode with <= 16 rows (attn_decode_kernel): one round (256 slots), at least
     //    ~32 blocks per split (4 per wave), at most 64 splits.  Its eight waves stream
     //    blocks on their own, so one long item per CU beats two shorter ones.
@@ -808,20 +809,23 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
     }
     const double item_blocks = total / slots;
     if (!dec && forced <= 0) {
-        // attn_fwd_kernel: one split count for every request, sized so the launch has about
-        // `slots` work items.  Splitting in proportion to each request's blocks measured
-        // slower on ragged batches (config 4: 380 vs 319 us sparse, 2386 vs 2077 us dense),
-        // and the blocks a request selects are device data the host does not see.
-        const int units = s.B * s.Hkv * ntiles;
-        forced = static_cast<int>(slots / (double)units + 0.5);
-        forced = min(forced, max(1, nkb_max / min_blocks));
-        forced = max(1, min(forced, max_splits));
-        // Requests of one length whose row tiles already fill three quarters of the CUs run
-        // unsplit: the items stay balanced and the split partials and their merge are saved
-        // (config-3 chunks, 256 tiles: 21 us of merge per layer).  Ragged batches keep the
-        // split, which balances their long rows against the short ones.
+        // attn_fwd_kernel: one split count for every request.  Splitting in proportion to
+        // each request's blocks measured slower on ragged batches (config 4: 380 vs 319 us
+        // sparse, 2386 vs 2077 us dense), and the blocks a request selects are device data
+        // the host does not see.
+        //  - Requests of one length: about one round of work items (one per CU).  Their rows'
+        //    lists have near-equal lengths, so the items stay balanced, and fewer splits
+        //    write fewer partials for the merge (config 2, 128 row tiles: 2 splits 513 us,
+        //    4 splits 522 us, 8 splits 549 us).  Row tiles that fill three quarters of the
+        //    CUs run unsplit (config-3 chunks, 256 tiles: no partials or merge).
+        //  - Ragged batches: about two rounds, which balances their long rows against the
+        //    short ones.
         bool same_len = true;
         for (int b = 1; b < s.B; ++b) same_len = same_len && nkb[b] == nkb[0];
+        const int units = s.B * s.Hkv * ntiles;
+        forced = static_cast<int>((same_len ? 256 : slots) / (double)units + 0.5);
+        forced = min(forced, max(1, nkb_max / min_blocks));
+        forced = max(1, min(forced, max_splits));
         if (same_len && units * 4 >= 3 * 256) forced = 1;
     }
     plan->max = 1;
