@@ -283,16 +283,6 @@ __device__ __forceinline__ int wave_sum_int(int v) {
     return v;
 }
 
-__device__ __forceinline__ int wave_excl_scan(int v, int lane) {
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int y = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += y;
-    }
-    return incl - v;
-}
-
 // The per-row selection runs one 256-thread workgroup per (b, h, qb) row; the row lives in
 // LDS.  Top-k is exact on the order (score desc, block id asc):
 //  1. a lower bound T_lo of the k-th largest key: the k-th largest of the 64 lane maxima

@@ -209,10 +209,10 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
  * causal masking (key position j visible iff j <= 64*P_b + t).  out has q's layout;
  * lse (optional, [B, Hq, q_len] fp32, natural log) receives the log-sum-exp.
  * num_splits >= 1 splits every row's block list that many ways; num_splits = 0 picks one
- * count for the launch, sized to about 512 work items (row tiles x splits) with at least
- * ~16 blocks per split, or 1 when all requests have one length and their row tiles fill
- * three quarters of the 256 CUs (ca_attn_pick_splits).  Whole KV rows are placed on the XCDs
- * longest-first either way.  More than one split needs a workspace of
+ * count for the launch (ca_attn_pick_splits) with at least ~16 blocks per split: about 256
+ * work items (row tiles x splits, one per CU) when all requests have one length, 1 when
+ * their row tiles alone fill three quarters of the 256 CUs, and about 512 for ragged
+ * batches.  Whole KV rows are placed on the XCDs longest-first either way.  More than one split needs a workspace of
  * ca_attn_workspace_size(dims, past, num_splits) bytes.
  * Replaces: flash_attn_with_kvcache / FlashInfer paged prefill as driven by
  * flash_attn_indexed_prefill_from_paged_kv (compact_attn/kernels/varlen/
