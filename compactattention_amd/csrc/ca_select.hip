@@ -166,11 +166,16 @@ __global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, Pas
 // over d = 0..127.
 constexpr int kPadRow = kD + 4;  // LDS row pitch (floats) for summary tiles
 
+// One workgroup computes a 64-row x KT-key tile of logits (KT = 32: twice the workgroups of
+// 64-key tiles, so the last round of the grid carries half as much work per CU).
+template <int KT>
 __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float* qhat, const float* khat,
                                                            float scale, PastBlocks pb, float* logits) {
+    static_assert(KT == 32 || KT == 64, "16 key groups of KT/16 keys");
+    constexpr int KJ = KT / 16;  // keys per thread
     __shared__ __attribute__((aligned(16))) float qt[64 * kPadRow];
-    __shared__ __attribute__((aligned(16))) float kt[64 * kPadRow];
-    const int kb0 = blockIdx.x * 64;
+    __shared__ __attribute__((aligned(16))) float kt[KT * kPadRow];
+    const int kb0 = blockIdx.x * KT;
     const int row = blockIdx.y;
     const int m0 = blockIdx.z * 64;
     const int b = row / s.Hkv;
@@ -183,47 +188,58 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
     const float* qbase = qhat + ((int64_t)(b * s.Hq + hk * s.G) * s.Qb + m0) * kD;
     const float* kbase = khat + ((int64_t)row * s.cap + kb0) * kD;
     const int mrows = min(64, M - m0);
-    const int krows = min(64, nkb - kb0);
+    const int krows = min(KT, nkb - kb0);
     {
-        // all 16 loads of a thread in flight before the LDS stores
-        constexpr int kIters = 64 * (kD / 4) / 256;
-        float4 qv[kIters], kv[kIters];
+        // all loads of a thread in flight before the LDS stores
+        constexpr int kQIters = 64 * (kD / 4) / 256;
+        constexpr int kKIters = KT * (kD / 4) / 256;
+        float4 qv[kQIters], kv[kKIters];
 #pragma unroll
-        for (int i = 0; i < kIters; ++i) {
+        for (int i = 0; i < kQIters; ++i) {
             const int f = t + 256 * i;
             const int r = f >> 5, c4 = f & 31;
             qv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            kv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (r < mrows) qv[i] = *reinterpret_cast<const float4*>(qbase + (int64_t)r * kD + c4 * 4);
+        }
+#pragma unroll
+        for (int i = 0; i < kKIters; ++i) {
+            const int f = t + 256 * i;
+            const int r = f >> 5, c4 = f & 31;
+            kv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (r < krows) kv[i] = *reinterpret_cast<const float4*>(kbase + (int64_t)r * kD + c4 * 4);
         }
 #pragma unroll
-        for (int i = 0; i < kIters; ++i) {
+        for (int i = 0; i < kQIters; ++i) {
             const int f = t + 256 * i;
             const int r = f >> 5, c4 = f & 31;
             *reinterpret_cast<float4*>(qt + r * kPadRow + c4 * 4) = qv[i];
+        }
+#pragma unroll
+        for (int i = 0; i < kKIters; ++i) {
+            const int f = t + 256 * i;
+            const int r = f >> 5, c4 = f & 31;
             *reinterpret_cast<float4*>(kt + r * kPadRow + c4 * 4) = kv[i];
         }
     }
     __syncthreads();
     const int lane = t & 63;
     const int tm = lane & 15;              // query rows tm + 16 i
-    const int tn = (t >> 6) * 4 + (lane >> 4);  // key rows 4 tn + j
-    float acc[4][4];
+    const int tn = (t >> 6) * 4 + (lane >> 4);  // key rows KJ tn + j
+    float acc[4][KJ];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = 0.0f;
+        for (int j = 0; j < KJ; ++j) acc[i][j] = 0.0f;
     for (int d = 0; d < kD; d += 4) {
-        float4 a[4], c[4];
+        float4 a[4], c[KJ];
 #pragma unroll
         for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const float4*>(qt + (tm + 16 * i) * kPadRow + d);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) c[j] = *reinterpret_cast<const float4*>(kt + (4 * tn + j) * kPadRow + d);
+        for (int j = 0; j < KJ; ++j) c[j] = *reinterpret_cast<const float4*>(kt + (KJ * tn + j) * kPadRow + d);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < KJ; ++j) {
                 float v = acc[i][j];
                 v = __builtin_fmaf(a[i].x, c[j].x, v);
                 v = __builtin_fmaf(a[i].y, c[j].y, v);
@@ -239,8 +255,8 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
         const int qb = m % s.Qb;
         float* out = logits + ((int64_t)(b * s.Hq + hk * s.G) * s.Qb + m) * s.cap;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int kb = kb0 + 4 * tn + j;
+        for (int j = 0; j < KJ; ++j) {
+            const int kb = kb0 + KJ * tn + j;
             if (kb <= P + qb) out[kb] = acc[i][j] * scale;
         }
     }
@@ -793,8 +809,9 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
     if (compute) {
         int max_nkb = 0;
         for (int b = 0; b < s.B; ++b) max_nkb = max(max_nkb, pb.p[b] + s.Qb);
-        dim3 grid((max_nkb + 63) / 64, s.B * s.Hkv, (s.G * s.Qb + 63) / 64);
-        hipLaunchKernelGGL(block_logits_kernel, grid, dim3(256), 0, stream, s, qhat, khat, scale, pb, scores);
+        constexpr int kKT = 32;
+        dim3 grid((max_nkb + kKT - 1) / kKT, s.B * s.Hkv, (s.G * s.Qb + 63) / 64);
+        hipLaunchKernelGGL(block_logits_kernel<kKT>, grid, dim3(256), 0, stream, s, qhat, khat, scale, pb, scores);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
