@@ -471,21 +471,28 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     for (int sp0 = 0; sp0 < nsplit; sp0 += 8) {
         float4 o[8];
         float wgt[8];
+        // the partials' loads do not wait for the weights; a split with weight 0 (no keys)
+        // is dropped by a select, so whatever its slot holds never reaches the sum
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int sp = sp0 + u;
+            o[u] = sp < nsplit ? *reinterpret_cast<const float4*>(wo + (int64_t)sp * rows_all * 128)
+                               : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int sp = sp0 + u;
             const float wa = __shfl(w0, sp & 31, 32);
             const float wb = __shfl(w1, sp & 31, 32);
             wgt[u] = sp < nsplit ? (sp < 32 ? wa : wb) : 0.0f;
-            o[u] = wgt[u] != 0.0f ? *reinterpret_cast<const float4*>(wo + (int64_t)sp * rows_all * 128)
-                                  : float4{0.0f, 0.0f, 0.0f, 0.0f};
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            acc.x += wgt[u] * o[u].x;
-            acc.y += wgt[u] * o[u].y;
-            acc.z += wgt[u] * o[u].z;
-            acc.w += wgt[u] * o[u].w;
+            const bool use = wgt[u] != 0.0f;
+            acc.x += use ? wgt[u] * o[u].x : 0.0f;
+            acc.y += use ? wgt[u] * o[u].y : 0.0f;
+            acc.z += use ? wgt[u] * o[u].z : 0.0f;
+            acc.w += use ? wgt[u] * o[u].w : 0.0f;
         }
     }
     const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
