@@ -29,6 +29,7 @@ CA_ERR_HIP = -4
 RULE_TOPK = 1
 RULE_ALPHA = 2
 RULE_THRESHOLD = 4
+RULE_TOPK_ALLCOLS = 8
 
 EXPORTED = (
     "ca_abi_version",

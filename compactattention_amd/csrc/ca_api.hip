@@ -163,8 +163,10 @@ int check_rope(const float* c, const float* s, int64_t rows, int max_nkb) {
 
 int check_rule(const ca_select_rule* r) {
     if (r == nullptr) return fail(CA_ERR_INVALID, "rule is NULL");
-    if (r->flags & ~(CA_RULE_TOPK | CA_RULE_ALPHA | CA_RULE_THRESHOLD))
+    if (r->flags & ~(CA_RULE_TOPK | CA_RULE_ALPHA | CA_RULE_THRESHOLD | CA_RULE_TOPK_ALLCOLS))
         return fail(CA_ERR_INVALID, "unknown rule flags 0x%x", r->flags);
+    if ((r->flags & CA_RULE_TOPK_ALLCOLS) && !(r->flags & CA_RULE_TOPK))
+        return fail(CA_ERR_INVALID, "CA_RULE_TOPK_ALLCOLS needs CA_RULE_TOPK");
     if ((r->flags & CA_RULE_TOPK) && r->topk < 0) return fail(CA_ERR_INVALID, "topk=%d < 0", r->topk);
     return CA_OK;
 }

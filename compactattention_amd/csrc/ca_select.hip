@@ -369,6 +369,7 @@ __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p)
     extern __shared__ float row[];  // [cap]
     __shared__ float red_f[kSelWaves];
     __shared__ int red_i[kSelWaves];
+    __shared__ int red_z[kSelWaves];
     __shared__ uint32_t tmax[kSelThreads];
     __shared__ uint32_t cand_key[kCandCap];
     __shared__ int cand_id[kCandCap];
@@ -465,34 +466,60 @@ __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p)
     }
     __syncthreads();
 
-    // Row statistics: finite causal max (alpha rule), finite past count and the per-thread
-    // maximum past key (top-k bound).
+    // Row statistics: the alpha rule's row max, the top-k candidate count and the
+    // per-thread maximum candidate key (top-k bound).
+    //  - Row max: the max over all Kb = P + Qb columns of the zeroed row, where non-causal
+    //    and non-finite entries read as 0 (flashprefill_prefill.py:633-645).
+    //  - Top-k candidates: the finite past blocks kb < P (past-only form), or every column
+    //    kb < Kb with its zeroed value (CA_RULE_TOPK_ALLCOLS, the reference's min_budget:
+    //    torch.topk over the zeroed row, :637-643); picks past the causal edge are dropped.
     const ca_select_rule& rule = p.rule;
-    const bool use_topk = (rule.flags & CA_RULE_TOPK) && rule.topk > 0 && P > 0;
+    const int Kb = P + s.Qb;
+    const bool all_cols = (rule.flags & CA_RULE_TOPK_ALLCOLS) != 0;
+    const int kend = all_cols ? Kb : P;
+    const bool use_topk = (rule.flags & CA_RULE_TOPK) && rule.topk > 0 && kend > 0;
+    auto cand_val = [&](int kb, float& v) -> bool {
+        if (all_cols) {
+            v = kb < n ? row[kb] : 0.0f;
+            if (!is_finite_f(v)) v = 0.0f;
+            return true;
+        }
+        v = row[kb];
+        return is_finite_f(v);
+    };
     {
-        float mx = 0.0f;
-        int nc = 0;
+        float mx = kNegInf;
+        int nc = 0, nz = 0;
         uint32_t kmax = 0;
-        for (int kb = t; kb < n; kb += kSelThreads) {
-            const float v = row[kb];
-            if (!is_finite_f(v)) continue;
-            mx = fmaxf(mx, v);
-            if (kb < P) {
+        const int lim = max(n, use_topk ? kend : 0);
+        for (int kb = t; kb < lim; kb += kSelThreads) {
+            if (kb < n) {
+                const float v = row[kb];
+                if (is_finite_f(v))
+                    mx = fmaxf(mx, v);
+                else
+                    ++nz;
+            }
+            float cv;
+            if (use_topk && kb < kend && cand_val(kb, cv)) {
                 ++nc;
-                kmax = max(kmax, order_key(v));
+                kmax = max(kmax, order_key(cv));
             }
         }
         mx = wave_max(mx);
         nc = wave_sum_int(nc);
+        nz = wave_sum_int(nz);
         tmax[t] = kmax;
         if (lane == 0) {
             red_f[wave] = mx;
             red_i[wave] = nc;
+            red_z[wave] = nz;
         }
         if (t == 0) cand_n = 0;
     }
     __syncthreads();
-    const float rowmax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    float rowmax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    if (n < Kb || red_z[0] + red_z[1] + red_z[2] + red_z[3] > 0) rowmax = fmaxf(rowmax, 0.0f);
     const int ncand = red_i[0] + red_i[1] + red_i[2] + red_i[3];
     const float alpha_cut = rule.alpha * rowmax;
     const bool take_all = use_topk && rule.topk >= ncand;
@@ -511,9 +538,9 @@ __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p)
         }
         __syncthreads();
         const uint32_t lo = sel_lo;
-        for (int kb = t; kb < P; kb += kSelThreads) {
-            const float v = row[kb];
-            if (!is_finite_f(v)) continue;
+        for (int kb = t; kb < kend; kb += kSelThreads) {
+            float v;
+            if (!cand_val(kb, v)) continue;
             const uint32_t key = order_key(v);
             if (key < lo) continue;
             const int slot = atomicAdd(&cand_n, 1);
@@ -537,26 +564,26 @@ __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p)
                 for (int bit = 31; bit >= 0; --bit) {
                     const uint32_t c = T | (1u << bit);
                     int cnt = 0;
-                    for (int kb = lane; kb < P; kb += 64) {
-                        const float v = row[kb];
-                        cnt += (is_finite_f(v) && order_key(v) >= c) ? 1 : 0;
+                    for (int kb = lane; kb < kend; kb += 64) {
+                        float v;
+                        cnt += (cand_val(kb, v) && order_key(v) >= c) ? 1 : 0;
                     }
                     if (wave_sum_int(cnt) >= k) T = c;
                 }
                 int gt = 0;
-                for (int kb = lane; kb < P; kb += 64) {
-                    const float v = row[kb];
-                    gt += (is_finite_f(v) && order_key(v) > T) ? 1 : 0;
+                for (int kb = lane; kb < kend; kb += 64) {
+                    float v;
+                    gt += (cand_val(kb, v) && order_key(v) > T) ? 1 : 0;
                 }
                 const int krem = k - wave_sum_int(gt);
                 // the krem-th key equal to T in ascending block order
                 const uint64_t lt_mask = (1ull << lane) - 1ull;
                 int seen = 0;
-                eq_cut = P;
-                for (int base = 0; base < P; base += 64) {
+                eq_cut = kend;
+                for (int base = 0; base < kend; base += 64) {
                     const int kb = base + lane;
-                    const float v = kb < P ? row[kb] : 0.0f;
-                    const bool e = kb < P && is_finite_f(v) && order_key(v) == T;
+                    float v = 0.0f;
+                    const bool e = kb < kend && cand_val(kb, v) && order_key(v) == T;
                     const uint64_t bal = __ballot(e);
                     const int cnt = __popcll(bal);
                     if (seen + cnt >= krem) {
@@ -590,11 +617,12 @@ __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p)
             if (kb < rule.sink_blocks) keep = true;
             if (qabs - kb < rule.window_blocks) keep = true;
             if (kb < P && kb >= P - rule.local_blocks) keep = true;
-            if (use_topk && kb < P && fin) {
+            float cv;
+            if (use_topk && kb < kend && cand_val(kb, cv)) {
                 if (take_all) {
                     keep = true;
                 } else {
-                    const uint32_t key = order_key(v);
+                    const uint32_t key = order_key(cv);
                     if (key > T || (key == T && kb <= eq_cut)) keep = true;
                 }
             }

@@ -5,7 +5,9 @@ Mirrors flashprefill_compactattn_prefill_full_kv of the reference
 return value -- with the selection of _flashprefill_keep_block_from_scores_rowwise
 (:596-666): per (Q head, query block) row, keep score >= alpha * rowmax, the sink blocks
 (kb < attention_sink), the window (0 <= q_abs - kb < window_size) and, with min_budget > 0,
-the top-min_budget past blocks by (score desc, block id asc); rows of the last
+the top-min_budget columns of the row by (score desc, block id asc), ranked over all Kb key
+blocks with non-causal and non-finite entries read as 0 (torch.topk over the zeroed row,
+:633-647; picks past the causal edge are dropped); rows of the last
 last_n_block query blocks stay out of the union; the current chunk is always kept; then
 the GQA union, int32 block tables and the indexed attention.
 
@@ -31,7 +33,7 @@ from .attention_forward_chunked_dense import CACHE_FILL_BACKENDS, PACK_IMPLS
 def flashprefill_rule(attention_sink: int, window_size: int, alpha: float, last_n_block: int,
                       min_budget: int) -> ops.Rule:
     return ops.Rule(topk=max(int(min_budget), 0), alpha=float(alpha), sink_blocks=int(attention_sink),
-                    window_blocks=int(window_size), last_n_block=int(last_n_block))
+                    window_blocks=int(window_size), last_n_block=int(last_n_block), topk_all_columns=True)
 
 
 def flashprefill_compactattn_prefill_full_kv(

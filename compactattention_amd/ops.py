@@ -22,7 +22,11 @@ class Rule:
     """Block selection rule (``ca_select_rule``).
 
     topk       keep the top-k past blocks of every (head, query block) row, ordered by
-               (score desc, block id asc) -- the reference's ``min_budget``;
+               (score desc, block id asc);
+    topk_all_columns
+               rank every column kb < P + Qb instead (non-causal and non-finite entries
+               read as 0) and keep the causal picks -- the reference's ``min_budget``
+               (torch.topk over the zeroed row, flashprefill_prefill.py:633-647);
     alpha      keep blocks with score >= alpha * row max (FlashPrefill);
     threshold  keep blocks with score > threshold (SeerAttention, strict);
     sink_blocks / window_blocks / local_blocks / last_n_block as in ``ca_select_rule``.
@@ -35,11 +39,14 @@ class Rule:
     window_blocks: int = 0
     local_blocks: int = 0
     last_n_block: int = 0
+    topk_all_columns: bool = False
 
     def to_c(self) -> SelectRule:
         flags = 0
         if self.topk > 0:
             flags |= _hip.RULE_TOPK
+            if self.topk_all_columns:
+                flags |= _hip.RULE_TOPK_ALLCOLS
         if self.alpha is not None:
             flags |= _hip.RULE_ALPHA
         if self.threshold is not None:

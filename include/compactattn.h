@@ -49,8 +49,16 @@ enum {
 
 /* Selection-rule flags. */
 #define CA_RULE_TOPK 1      /* keep the top-k past blocks by (score desc, block id asc)   */
-#define CA_RULE_ALPHA 2     /* keep score >= alpha * row max (row max over causal, >= 0) */
+#define CA_RULE_ALPHA 2     /* keep score >= alpha * row max                              */
 #define CA_RULE_THRESHOLD 4 /* keep score > threshold (strict)                           */
+/* With CA_RULE_TOPK: rank every column kb < P + Qb instead of the past blocks only, each by
+ * its value in the zeroed row (non-causal and non-finite entries read as 0), and keep the
+ * picks that are causal -- the reference's min_budget (torch.topk over the zeroed row,
+ * compact_attn/modules/flashprefill_prefill.py:633-647).  Ties go to the lower block id. */
+#define CA_RULE_TOPK_ALLCOLS 8
+
+/* The alpha rule's row max is the max over all P + Qb columns of the zeroed row, as in
+ * flashprefill_prefill.py:633-645 (0 whenever a non-causal or non-finite column exists). */
 
 typedef struct {
     int32_t batch;        /* requests in the launch, <= CA_MAX_BATCH                 */

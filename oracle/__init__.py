@@ -25,6 +25,7 @@ _LIB_PATH = os.path.join(_HERE, "libca_oracle.so")
 RULE_TOPK = 1
 RULE_ALPHA = 2
 RULE_THRESHOLD = 4
+RULE_TOPK_ALLCOLS = 8
 D = 128
 BLOCK = 64
 
@@ -53,11 +54,14 @@ class Rule:
     window_blocks: int = 0
     local_blocks: int = 0
     last_n_block: int = 0
+    topk_all_columns: bool = False  # rank all Kb columns (the reference's min_budget)
 
     def to_c(self) -> _Rule:
         flags = 0
         if self.topk > 0:
             flags |= RULE_TOPK
+            if self.topk_all_columns:
+                flags |= RULE_TOPK_ALLCOLS
         if self.alpha is not None:
             flags |= RULE_ALPHA
         if self.threshold is not None:

@@ -16,8 +16,9 @@
  *                      compact_attn/prefill_sparse/llama/modeling_llama_seerattn.py:968-1024
  *                      (block causal mask kb <= floor(q_block_end / 64)); FlashPrefill's
  *                      normalisation over key blocks flashprefill_native_forward.py:365-374.
- *   orc_select_rows    compact_attn/modules/flashprefill_prefill.py:596-666 (alpha, sink,
- *                      window, min_budget top-k, causal), and the Seer threshold rule
+ *   orc_select_rows    compact_attn/modules/flashprefill_prefill.py:596-666 (alpha over the
+ *                      zeroed row :633-645, sink, window, min_budget top-k over all Kb columns
+ *                      :637-643, causal :647; and a past-only top-k form), and the Seer rule
  *                      compact_attn/modules/attention_forward_chunked_dense.py:352-403
  *                      (max over valid query blocks > threshold, strict).
  *   orc_union_compact  attention_forward_chunked_dense.py:641-683 (GQA union, current chunk
@@ -188,11 +189,21 @@ static int key_greater(float a, int ia, float b, int ib) {
     return ia < ib;
 }
 
+/* Value of column kb in the reference's zeroed row (flashprefill_prefill.py:633-634):
+ * non-causal (kb > qabs) and non-finite entries read as +0, and -0 is +0. */
+static inline float zeroed_value(const float* s, int kb, int n) {
+    if (kb >= n || !isfinite(s[kb])) return 0.0f;
+    return s[kb] == 0.0f ? 0.0f : s[kb];
+}
+
 void orc_select_rows(const float* scores, int B, int Hq, int Qb, int cap,
                      const int32_t* past_blocks, const orc_rule* rule, uint8_t* rowkeep) {
     int* cand = (int*)malloc(sizeof(int) * (size_t)(cap > 0 ? cap : 1));
+    float* val = (float*)malloc(sizeof(float) * (size_t)(cap > 0 ? cap : 1));
+    const int all_cols = (rule->flags & ORC_RULE_TOPK_ALLCOLS) != 0;
     for (int b = 0; b < B; ++b) {
         const int P = past_blocks[b];
+        const int Kb = P + Qb;
         for (int h = 0; h < Hq; ++h)
             for (int qb = 0; qb < Qb; ++qb) {
                 const float* s = scores + (((int64_t)b * Hq + h) * Qb + qb) * cap;
@@ -200,9 +211,12 @@ void orc_select_rows(const float* scores, int B, int Hq, int Qb, int cap,
                 const int qabs = P + qb;
                 const int n = qabs + 1; /* causal columns */
                 memset(out, 0, (size_t)cap);
-                float rowmax = 0.0f;
-                for (int kb = 0; kb < n; ++kb)
-                    if (isfinite(s[kb]) && s[kb] > rowmax) rowmax = s[kb];
+                /* alpha rule: the max over all Kb columns of the zeroed row (:633-645) */
+                float rowmax = zeroed_value(s, 0, n);
+                for (int kb = 1; kb < Kb; ++kb) {
+                    const float v = zeroed_value(s, kb, n);
+                    if (v > rowmax) rowmax = v;
+                }
                 const float alpha_cut = rule->alpha * rowmax;
                 for (int kb = 0; kb < n; ++kb) {
                     int keep = 0;
@@ -215,24 +229,39 @@ void orc_select_rows(const float* scores, int B, int Hq, int Qb, int cap,
                     out[kb] = (uint8_t)keep;
                 }
                 if ((rule->flags & ORC_RULE_TOPK) && rule->topk > 0) {
-                    /* top-k over finite past blocks by (-score, index): selection by repeated
-                     * extraction of the best remaining candidate. */
+                    /* Candidates by (-score, index), taken by repeated extraction of the best
+                     * remaining one.
+                     *  - past-only form: the finite past blocks kb < P;
+                     *  - all-columns form (the reference's min_budget, torch.topk over the Kb
+                     *    columns of the zeroed row, :637-643): every kb < Kb with its zeroed
+                     *    value; picks past the causal edge are dropped by the causal mask (:647). */
                     int nc = 0;
-                    for (int kb = 0; kb < P && kb < n; ++kb)
-                        if (isfinite(s[kb])) cand[nc++] = kb;
+                    if (all_cols) {
+                        for (int kb = 0; kb < Kb; ++kb) {
+                            val[kb] = zeroed_value(s, kb, n);
+                            cand[nc++] = kb;
+                        }
+                    } else {
+                        for (int kb = 0; kb < P && kb < n; ++kb)
+                            if (isfinite(s[kb])) {
+                                val[kb] = s[kb] == 0.0f ? 0.0f : s[kb];
+                                cand[nc++] = kb;
+                            }
+                    }
                     const int k = rule->topk < nc ? rule->topk : nc;
                     for (int i = 0; i < k; ++i) {
                         int best = i;
                         for (int j = i + 1; j < nc; ++j)
-                            if (key_greater(s[cand[j]], cand[j], s[cand[best]], cand[best])) best = j;
+                            if (key_greater(val[cand[j]], cand[j], val[cand[best]], cand[best])) best = j;
                         const int tmp = cand[i];
                         cand[i] = cand[best];
                         cand[best] = tmp;
-                        out[cand[i]] = 1;
+                        if (cand[i] < n) out[cand[i]] = 1;
                     }
                 }
             }
     }
+    free(val);
     free(cand);
 }
 

@@ -28,6 +28,7 @@ extern "C" {
 #define ORC_RULE_TOPK 1
 #define ORC_RULE_ALPHA 2
 #define ORC_RULE_THRESHOLD 4
+#define ORC_RULE_TOPK_ALLCOLS 8 /* with ORC_RULE_TOPK: rank all Kb columns (the reference's min_budget) */
 
 typedef struct {
     int32_t flags;

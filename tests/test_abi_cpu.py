@@ -150,9 +150,13 @@ def test_table_to_csr_validation():
 def test_rule_and_select_validation():
     lib = _hip.lib()
     d = _dims()
-    bad = _hip.SelectRule(8, 0, 0.0, 0.0, 0, 0, 0, 0)
+    bad = _hip.SelectRule(16, 0, 0.0, 0.0, 0, 0, 0, 0)
     rc = lib.ca_select_scores(ctypes.byref(d), FAKE, 0, 0, 0, 0, ctypes.byref(bad), _past(2), FAKE, None)
     assert rc == _hip.CA_ERR_INVALID and "flags" in _hip.last_error()
+    # the all-columns modifier needs the top-k rule itself
+    lone = _hip.SelectRule(_hip.RULE_TOPK_ALLCOLS, 3, 0.0, 0.0, 0, 0, 0, 0)
+    rc = lib.ca_select_scores(ctypes.byref(d), FAKE, 0, 0, 0, 0, ctypes.byref(lone), _past(2), FAKE, None)
+    assert rc == _hip.CA_ERR_INVALID and "CA_RULE_TOPK" in _hip.last_error()
     neg = _hip.SelectRule(_hip.RULE_TOPK, -1, 0.0, 0.0, 0, 0, 0, 0)
     rc = lib.ca_select_scores(ctypes.byref(d), FAKE, 0, 0, 0, 0, ctypes.byref(neg), _past(2), FAKE, None)
     assert rc == _hip.CA_ERR_INVALID

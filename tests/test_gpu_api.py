@@ -13,15 +13,18 @@ import pytest
 import torch
 
 import oracle
-from compactattention_amd.flashprefill_vendor import flash_prefill_compute_mean_k, flash_prefill_score_chunked_from_mean_k
+from compactattention_amd import ops
+from compactattention_amd.flashprefill_vendor import (flash_prefill_compute_mean_k,
+                                                      flash_prefill_score_chunked_from_mean_k, mean_k_kernel_layout)
 from compactattention_amd.kv_cache import PagedKVCache
 from compactattention_amd.modules.attention_forward_chunked_dense import (
     chunked_prefill_column_dense_attention_forward, chunked_prefill_column_dense_attention_from_keep_block)
-from compactattention_amd.modules.flashprefill_prefill import flashprefill_compactattn_prefill_full_kv
+from compactattention_amd.modules.flashprefill_prefill import (flashprefill_compactattn_prefill_full_kv,
+                                                               flashprefill_rule)
 from compactattention_amd.prefill_sparse.attn_gate import AttnGate
 from compactattention_amd.synthetic import make_chunk, rope_tables
 
-from .util import bits, f32, float_bits_equal
+from .util import bits, f32, float_bits_equal, ref_flashprefill_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -93,8 +96,16 @@ def test_from_keep_block_matches_union(gpu):
 @pytest.mark.parametrize("params", [
     dict(attention_sink=2, window_size=4, alpha=0.06, last_n_block=2, min_budget=0),
     dict(attention_sink=1, window_size=0, alpha=0.5, last_n_block=0, min_budget=6),
+    dict(attention_sink=2, window_size=4, alpha=0.06, last_n_block=1, min_budget=12),
+    dict(attention_sink=0, window_size=2, alpha=0.9, last_n_block=0, min_budget=30),
 ])
 def test_flashprefill_entry(gpu, params):
+    """The entry's tables (through the rule it builds, flashprefill_rule) and its output
+    against the reference's selection semantics: a torch restatement of
+    _flashprefill_keep_block_from_scores_rowwise (flashprefill_prefill.py:596-666, min_budget
+    by torch.topk over all Kb columns of the zeroed row) applied to the fp32 scores, which
+    the GPU reproduces bit for bit.  The scores are continuous, so the only ties are the
+    zeroed non-causal columns, which the causal mask drops whichever torch.topk picks."""
     _print_case(test="flashprefill_entry", **params)
     Hq, Hkv, Lq, past = 8, 2, 256, 64 * 40
     ch = make_chunk([past], Lq, Hq, Hkv, seed=5)
@@ -108,11 +119,24 @@ def test_flashprefill_entry(gpu, params):
     khat = oracle.block_mean(bits(_seq_first(ch.k)))
     qhat = oracle.block_mean(bits(ch.q))
     sc = oracle.block_scores(qhat, khat, P, SCALE)
+    ref_table, ref_counts = ref_flashprefill_tables(sc, P, Hkv, params["alpha"], params["attention_sink"],
+                                                    params["window_size"], params["min_budget"],
+                                                    params["last_n_block"])
+    # the oracle's all-columns rule is the same selection
     rule = oracle.Rule(topk=params["min_budget"], alpha=params["alpha"], sink_blocks=params["attention_sink"],
-                       window_blocks=params["window_size"], last_n_block=params["last_n_block"])
-    keep = oracle.select_rows(sc, P, rule)
-    _, _, table, counts = oracle.union_compact(keep, Hkv, P, params["last_n_block"])
-    _check_attention(out, ch, table, counts)
+                       window_blocks=params["window_size"], last_n_block=params["last_n_block"],
+                       topk_all_columns=True)
+    _, _, table, counts = oracle.union_compact(oracle.select_rows(sc, P, rule), Hkv, P, params["last_n_block"])
+    assert np.array_equal(counts, ref_counts) and np.array_equal(table, ref_table)
+    # the GPU tables through the entry's own rule
+    gqhat = ops.pool_query(ch.q.to(gpu), P, cap, num_kv_heads=Hkv)
+    grule = flashprefill_rule(params["attention_sink"], params["window_size"], params["alpha"],
+                              params["last_n_block"], params["min_budget"])
+    rowmask, _ = ops.score_select(gqhat, mean_k_kernel_layout(mean_k), SCALE, grule, P, Hkv, cap)
+    gtable, gcounts, _, _ = ops.union_compact(rowmask, P, Hkv, cap, last_n_block=params["last_n_block"])
+    assert np.array_equal(gcounts.cpu().numpy(), ref_counts)
+    assert np.array_equal(gtable.cpu().numpy(), ref_table)
+    _check_attention(out, ch, ref_table, ref_counts)
 
 
 def test_flashprefill_first_chunk_is_dense(gpu):

@@ -115,12 +115,18 @@ RULES = {
     "threshold": oracle.Rule(threshold=5e-3, sink_blocks=1, local_blocks=2),
     "topk_alpha": oracle.Rule(topk=3, alpha=0.5),
     "topk_ge_candidates": oracle.Rule(topk=1000),
+    # the reference's min_budget: top-k over all Kb columns of the zeroed row
+    "allcols_alpha_sink_window": oracle.Rule(topk=5, alpha=0.06, sink_blocks=2, window_blocks=4,
+                                             topk_all_columns=True),
+    "allcols_near_kb": oracle.Rule(topk=40, topk_all_columns=True),
+    "allcols_ge_kb": oracle.Rule(topk=1000, topk_all_columns=True),
 }
 
 
 def _ops_rule(r: oracle.Rule) -> ops.Rule:
     return ops.Rule(topk=r.topk, alpha=r.alpha, threshold=r.threshold, sink_blocks=r.sink_blocks,
-                    window_blocks=r.window_blocks, local_blocks=r.local_blocks, last_n_block=r.last_n_block)
+                    window_blocks=r.window_blocks, local_blocks=r.local_blocks, last_n_block=r.last_n_block,
+                    topk_all_columns=r.topk_all_columns)
 
 
 @pytest.mark.parametrize("rule_name", sorted(RULES))
@@ -160,18 +166,21 @@ def test_select_scores_ties_and_nonfinite(gpu, dtype):
     s[0, 2, 1, 9] = float("inf")
     s[0, 0, 0, 11] = -0.0
     s = s.to(dtype)
-    for rule in (oracle.Rule(topk=6), oracle.Rule(topk=6, alpha=0.9), oracle.Rule(threshold=0.3, sink_blocks=1)):
+    for rule in (oracle.Rule(topk=6), oracle.Rule(topk=6, alpha=0.9), oracle.Rule(threshold=0.3, sink_blocks=1),
+                 oracle.Rule(topk=6, alpha=0.5, topk_all_columns=True), oracle.Rule(topk=51, topk_all_columns=True)):
         rowmask = ops.select_scores(s.to(gpu), _ops_rule(rule), past, Hkv, cap, Lq)
         ref = oracle.select_rows(s.float().numpy(), past, rule)
         assert np.array_equal(unpack_rowmask(rowmask, cap), ref), rule
 
 
+@pytest.mark.parametrize("all_columns", [False, True])
 @pytest.mark.parametrize("case", ["two_values", "k_gt_64", "k_eq_64", "sparse_finite", "negative"])
-def test_select_topk_search_paths(gpu, case):
+def test_select_topk_search_paths(gpu, case, all_columns):
     """Top-k through each branch of the kernel's search: the candidate list after the
     lane-maximum bound (k <= 64), its overflow into the full-row search (heavy ties) and
-    k > 64; also rows where few lanes hold finite candidates and all-negative scores."""
-    _print_case(test="select_topk_paths", case=case)
+    k > 64; also rows where few lanes hold finite candidates and all-negative scores (where
+    the all-columns form ranks the zeroed non-causal columns above every causal one)."""
+    _print_case(test="select_topk_paths", case=case, all_columns=all_columns)
     B, Hkv, G, Lq = 1, 2, 2, 128
     Hq = Hkv * G
     past = [700]
@@ -195,10 +204,11 @@ def test_select_topk_search_paths(gpu, case):
         s = -torch.rand((B, Hq, qb, cap), generator=g) * 5
         s[..., 5] = -0.0
         s[..., 6] = 0.0
-    rule = oracle.Rule(topk=k)
+    rule = oracle.Rule(topk=k, topk_all_columns=all_columns)
     rowmask = ops.select_scores(s.to(gpu), _ops_rule(rule), past, Hkv, cap, Lq)
     ref = oracle.select_rows(s.numpy(), past, rule)
-    assert ref[..., :past[0]].sum(axis=-1).max() == k
+    if not all_columns:
+        assert ref[..., :past[0]].sum(axis=-1).max() == k
     assert np.array_equal(unpack_rowmask(rowmask, cap), ref)
 
 

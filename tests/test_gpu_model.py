@@ -236,7 +236,7 @@ def test_layer_tables_bit_exact(gpu, selector):
         rule = oracle.Rule(topk=c.seerattn_flashprefill_min_budget, alpha=c.seerattn_flashprefill_alpha,
                            sink_blocks=c.seerattn_flashprefill_attention_sink,
                            window_blocks=c.seerattn_flashprefill_window_size,
-                           last_n_block=c.seerattn_flashprefill_last_n_block)
+                           last_n_block=c.seerattn_flashprefill_last_n_block, topk_all_columns=True)
         last_n = c.seerattn_flashprefill_last_n_block
     keep = oracle.select_rows(scores, P, rule)
     _, _, table, counts = oracle.union_compact(keep, Hkv, P, last_n)

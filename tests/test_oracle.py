@@ -15,6 +15,8 @@ import torch
 
 import oracle
 
+from .util import ref_flashprefill_rowwise, ref_flashprefill_tables
+
 RNG = np.random.default_rng(1234)
 
 
@@ -154,6 +156,74 @@ def test_select_topk_brute_force_with_ties():
                     ref = np.zeros(cap, np.uint8)
                     ref[cands] = 1
                     assert np.array_equal(got[b, h, q], ref), (k, b, h, q)
+
+
+def test_select_min_budget_all_columns_matches_torch_topk():
+    """The all-columns top-k (the reference's min_budget) against torch.topk on tie-free rows:
+    continuous scores of both signs, no non-finite entries, so the only equal values are the
+    zeroed non-causal columns, which the causal mask drops whichever of them topk picks.
+    Negative scores put those zeros above causal entries (they use up budget) and make the
+    last query block's row max negative (no zeroed column in that row)."""
+    B, H, Qb = 2, 3, 4
+    past = [9, 17]
+    cap = max(past) + Qb + 3
+    for signed in (False, True):
+        s = RNG.standard_normal((B, H, Qb, cap)).astype(np.float32)
+        if not signed:
+            s = np.abs(s) + 0.01
+        else:
+            s[1, 2] = -np.abs(s[1, 2]) - 0.01  # all negative: a negative row max in the last block
+        for k in (0, 1, 3, 8, 15, 40):
+            for alpha in (0.0, 0.5, 1.5):
+                rule = oracle.Rule(topk=k, topk_all_columns=True, alpha=alpha, sink_blocks=1, window_blocks=2)
+                got = oracle.select_rows(s, past, rule)
+                for b in range(B):
+                    Kb = past[b] + Qb
+                    for h in range(H):
+                        ref = ref_flashprefill_rowwise(s[b, h, :, :Kb], past[b], alpha, 1, 2, k)
+                        assert np.array_equal(got[b, h, :, :Kb], ref), (signed, k, alpha, b, h)
+                        assert not got[b, h, :, Kb:].any()
+
+
+def test_select_min_budget_all_columns_ties_and_nonfinite():
+    """Ties (heavy), -0/+0, NaN and +-inf: the all-columns top-k equals a stable descending sort
+    of the zeroed row (ties to the lower block id), and a brute-force ranking by (-value, id)."""
+    B, H, Qb = 1, 2, 3
+    past = [12]
+    Kb = past[0] + Qb
+    s = (RNG.integers(-2, 4, (B, H, Qb, Kb)) * 0.25).astype(np.float32)
+    s[0, 0, 0, 2] = -0.0
+    s[0, 0, 1, 5] = np.nan
+    s[0, 1, 0, 7] = np.inf
+    s[0, 1, 2, 3] = -np.inf
+    for k in (1, 2, 5, 9, 14, 15, 30):
+        rule = oracle.Rule(topk=k, topk_all_columns=True, alpha=0.25)
+        got = oracle.select_rows(s, past, rule)
+        for h in range(H):
+            ref = ref_flashprefill_rowwise(s[0, h], past[0], 0.25, 0, 0, k, use_topk=False)
+            assert np.array_equal(got[0, h], ref), (k, h)
+            for q in range(Qb):
+                n = past[0] + q + 1
+                z = [float(s[0, h, q, kb]) if kb < n and np.isfinite(s[0, h, q, kb]) else 0.0 for kb in range(Kb)]
+                picks = sorted(range(Kb), key=lambda kb: (-(z[kb] + 0.0), kb))[:k]
+                for kb in picks:
+                    if kb < n:
+                        assert got[0, h, q, kb] == 1, (k, h, q, kb)
+
+
+def test_select_past_only_topk_differs_from_all_columns():
+    """The past-only top-k (this path's config-2 selector) spends the whole budget on past
+    blocks; the all-columns form lets current-chunk blocks take part of it."""
+    s = np.zeros((1, 1, 2, 12), np.float32)
+    s[0, 0, :, :10] = np.linspace(0.1, 0.2, 10, dtype=np.float32)
+    s[0, 0, :, 10:] = 1.0  # current-chunk blocks rank first
+    past = [10]
+    s[0, 0, 0, 11] = 0.0  # non-causal for query block 0
+    a = oracle.select_rows(s, past, oracle.Rule(topk=3))
+    b = oracle.select_rows(s, past, oracle.Rule(topk=3, topk_all_columns=True))
+    assert a[0, 0, 1, :10].sum() == 3 and set(np.nonzero(a[0, 0, 1])[0]) == {7, 8, 9}
+    assert set(np.nonzero(b[0, 0, 1])[0]) == {9, 10, 11}
+    assert set(np.nonzero(b[0, 0, 0])[0]) == {8, 9, 10}
 
 
 def test_select_local_blocks():
@@ -324,3 +394,17 @@ def test_planted_blocks_recalled_on_config0_shape():
     hits = sum(int(kv[0, h, blk]) for h in range(8) for blk in planted[h])
     recall = hits / sum(len(p) for p in planted)
     assert recall >= 0.5, recall
+
+
+def test_oracle_flashprefill_path_matches_reference_tables():
+    """Oracle selection + union with the all-columns top-k (and last_n_block) equals the
+    reference restatement's per-KV-group tables on continuous scores."""
+    B, Hq, Hkv, Qb = 2, 6, 2, 4
+    past = [11, 23]
+    cap = max(past) + Qb + 2
+    s = RNG.random((B, Hq, Qb, cap)).astype(np.float32) + 1e-3
+    for k, last_n in ((0, 0), (3, 1), (9, 2), (40, 0)):
+        rule = oracle.Rule(topk=k, topk_all_columns=True, alpha=0.4, sink_blocks=1, window_blocks=2, last_n_block=last_n)
+        _, _, tab, cnt = oracle.union_compact(oracle.select_rows(s, past, rule), Hkv, past, last_n)
+        rtab, rcnt = ref_flashprefill_tables(s, past, Hkv, 0.4, 1, 2, k, last_n)
+        assert np.array_equal(cnt, rcnt) and np.array_equal(tab, rtab), (k, last_n)

@@ -35,3 +35,62 @@ def pack_rowmask(keep: np.ndarray, cap: int) -> np.ndarray:
     padded[..., :cap] = keep
     w = (padded.reshape(keep.shape[:-1] + (words, 32)) << np.arange(32, dtype=np.uint64)).sum(-1)
     return w.astype(np.uint32)
+
+
+def ref_flashprefill_rowwise(scores_row, P, alpha, sink, window, min_budget, use_topk=True):
+    """Restatement of _flashprefill_keep_block_from_scores_rowwise (compact_attn/modules/
+    flashprefill_prefill.py:596-666) for one (request, Q head) slice of Kb = P + Qb columns:
+    the zeroed row (non-causal and non-finite entries 0), the alpha rule against the max of
+    that row, min_budget by torch.topk over all Kb columns, sink, window, causal mask.
+    Returns the per-query-block keep rows [Qb, Kb] (0/1).  With use_topk=False the top-k is
+    a stable descending sort (ties to the lower block id) instead of torch.topk."""
+    s = torch.as_tensor(np.asarray(scores_row), dtype=torch.float32)  # [Qb, Kb]
+    Qb, Kb = s.shape
+    k_ids = torch.arange(Kb).view(1, Kb)
+    q_ids = torch.arange(P, P + Qb).view(Qb, 1)
+    dist = q_ids - k_ids
+    causal = dist >= 0
+    finite = torch.isfinite(s) & causal
+    row = torch.where(finite, s, torch.zeros_like(s))
+    if min_budget > 0:
+        k = min(int(min_budget), Kb)
+        if use_topk:
+            vals, idx = torch.topk(row, k=k, dim=-1)
+        else:
+            vals, idx = torch.sort(row, dim=-1, descending=True, stable=True)
+            vals, idx = vals[:, :k], idx[:, :k]
+        mx = vals[:, :1]
+        keep = finite & (row >= mx * alpha)
+        keep.scatter_(-1, idx, True)
+    else:
+        mx = row.max(dim=-1, keepdim=True).values
+        keep = finite & (row >= mx * alpha)
+    keep = (keep | (k_ids < sink) | (causal & (dist < window))) & causal
+    return keep.numpy().astype(np.uint8)
+
+
+def ref_flashprefill_tables(scores, past, Hkv, alpha, sink, window, min_budget, last_n_block):
+    """Per-KV-group block tables from [B, Hq, Qb, >= P+Qb] scores through the reference's
+    rowwise rule (ref_flashprefill_rowwise), its Q-block union over the first
+    Qb - last_n_block query blocks (:609-610,648), current blocks kept, the GQA union
+    (:656-665) and ascending compaction.  Returns (table [B*Hkv, cap] -1 padded, counts)."""
+    B, Hq, Qb, cap = scores.shape
+    G = Hq // Hkv
+    tail = min(max(last_n_block, 0), Qb - 1) if Qb > 1 else 0
+    pooled = max(Qb - tail, 1)
+    table = np.full((B * Hkv, cap), -1, np.int32)
+    counts = np.zeros((B * Hkv,), np.int32)
+    for b in range(B):
+        P = int(past[b])
+        Kb = P + Qb
+        kq = np.zeros((Hq, Kb), bool)
+        for h in range(Hq):
+            rows = ref_flashprefill_rowwise(scores[b, h, :pooled, :Kb], P, alpha, sink, window, min_budget)
+            kq[h] = rows.any(axis=0)
+        kq[:, P:] = True
+        kv = kq.reshape(Hkv, G, Kb).any(axis=1)
+        for hk in range(Hkv):
+            ids = np.nonzero(kv[hk])[0]
+            table[b * Hkv + hk, :len(ids)] = ids
+            counts[b * Hkv + hk] = len(ids)
+    return table, counts
