@@ -15,7 +15,7 @@ from typing import Optional
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libcompactattn_hip.so")
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 HEAD_DIM = 128
 BLOCK = 64
 MAX_BATCH = 64
@@ -31,11 +31,17 @@ RULE_ALPHA = 2
 RULE_THRESHOLD = 4
 RULE_TOPK_ALLCOLS = 8
 
+POOL_MAX = 1
+POOL_MIN = 2
+POOL_AVG = 4
+
 EXPORTED = (
     "ca_abi_version",
     "ca_last_error",
     "ca_cache_fill",
     "ca_pool_query",
+    "ca_gate_key_summaries",
+    "ca_gate_query_summaries",
     "ca_score_select",
     "ca_select_scores",
     "ca_union_compact",
@@ -80,6 +86,7 @@ class KvLayout(ctypes.Structure):
         ("stride_tok", ctypes.c_int64),
         ("page_table", ctypes.c_void_p),
         ("page_table_stride", ctypes.c_int64),
+        ("num_pages", ctypes.c_int64),
     ]
 
 
@@ -117,6 +124,10 @@ _SIGNATURES = {
     "ca_cache_fill": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(SeqLayout), _P(KvLayout), _P(KvLayout),
                                      _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "ca_pool_query": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "ca_gate_key_summaries": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _i32, _vp, _i32, _vp, _vp, _i64, _vp,
+                                             _vp]),
+    "ca_gate_query_summaries": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _i32, _vp, _i32, _vp, _vp, _i64,
+                                               _vp, _vp]),
     "ca_score_select": (ctypes.c_int, [_P(Dims), _vp, _vp, _f32, _P(SelectRule), _vp, _vp, _vp, _vp]),
     "ca_select_scores": (ctypes.c_int, [_P(Dims), _vp, _i32, _i64, _i64, _i64, _P(SelectRule), _vp, _vp, _vp]),
     "ca_union_compact": (ctypes.c_int, [_P(Dims), _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),

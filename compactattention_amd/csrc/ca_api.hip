@@ -35,6 +35,8 @@ int hip_fail(hipError_t e, const char* what) {
     return fail(CA_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+constexpr int64_t kMaxStrideTok = int64_t{1} << 24;  // 64 rows x 2 bytes x stride_tok < 2^31
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned4(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3u) == 0; }
 
@@ -137,11 +139,18 @@ int check_kv(const ca_kv_layout* l, const char* name, int max_nkb, ca::KvAddr* o
     if (l->stride_b % 8 || l->stride_h % 8 || l->stride_blk % 8 || l->stride_tok % 8 || l->stride_tok <= 0 ||
         l->stride_b < 0 || l->stride_h < 0 || l->stride_blk < 0)
         return fail(CA_ERR_INVALID, "%s strides must be non-negative multiples of 8 (stride_tok > 0)", name);
+    // the kernels address a block's rows with 32-bit byte offsets (up to 64 * 2 * stride_tok)
+    if (l->stride_tok >= kMaxStrideTok)
+        return fail(CA_ERR_LIMIT, "%s stride_tok=%lld: a 64-token block must span < 2^31 bytes (stride_tok < %lld)",
+                    name, (long long)l->stride_tok, (long long)kMaxStrideTok);
     if (l->page_table != nullptr) {
         if (!aligned4(l->page_table)) return fail(CA_ERR_INVALID, "%s page_table misaligned", name);
         if (l->page_table_stride < max_nkb)
             return fail(CA_ERR_INVALID, "%s page_table_stride=%lld < blocks per row %d", name,
                         (long long)l->page_table_stride, max_nkb);
+        if (l->num_pages < 1 || l->num_pages > INT32_MAX)
+            return fail(CA_ERR_INVALID, "%s num_pages=%lld must be in [1, 2^31) with a page table", name,
+                        (long long)l->num_pages);
     }
     out->data = static_cast<uint16_t*>(l->data);
     out->sb = l->stride_b;
@@ -150,6 +159,7 @@ int check_kv(const ca_kv_layout* l, const char* name, int max_nkb, ca::KvAddr* o
     out->stok = l->stride_tok;
     out->page_table = l->page_table;
     out->pts = l->page_table_stride;
+    out->max_page = l->page_table != nullptr ? static_cast<int32_t>(l->num_pages - 1) : 0;
     return CA_OK;
 }
 
@@ -158,6 +168,12 @@ int check_rope(const float* c, const float* s, int64_t rows, int max_nkb) {
     if (c != nullptr && rows < max_nkb)
         return fail(CA_ERR_INVALID, "rope_rows=%lld < highest block id + 1 = %d", (long long)rows, max_nkb);
     if (c != nullptr && (!aligned4(c) || !aligned4(s))) return fail(CA_ERR_INVALID, "rope tables misaligned");
+    return CA_OK;
+}
+
+int check_pools(int32_t pools) {
+    if (pools <= 0 || (pools & ~(CA_POOL_MAX | CA_POOL_MIN | CA_POOL_AVG)))
+        return fail(CA_ERR_INVALID, "pools=0x%x must be a non-empty set of CA_POOL_MAX/MIN/AVG", pools);
     return CA_OK;
 }
 
@@ -207,8 +223,63 @@ int ca_cache_fill(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_
         if ((rc = check_rope(rope_cos, rope_sin, rope_rows, max_nkb)) != CA_OK) return rc;
     }
     hipError_t e = ca::launch_cache_fill(s, kn, vn, kc, vc, pb, kmean, gate_wk, rope_cos, rope_sin,
-                                         kgate, static_cast<hipStream_t>(stream));
+                                         kgate, CA_POOL_AVG, 1, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "cache_fill launch");
+    return ok();
+}
+
+int ca_gate_key_summaries(const ca_dims* dims, const ca_seq_layout* k_new, const int32_t* past_blocks_host,
+                          int32_t pools, const float* gate_wk, int32_t gate_heads, const float* rope_cos,
+                          const float* rope_sin, int64_t rope_rows, float* kgate, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    ca::SeqAddr kn{};
+    if ((rc = check_seq(k_new, "k_new", &kn)) != CA_OK) return rc;
+    if ((rc = check_pools(pools)) != CA_OK) return rc;
+    if (gate_wk == nullptr || kgate == nullptr) return fail(CA_ERR_INVALID, "gate_wk and kgate are required");
+    if (!aligned4(gate_wk) || !aligned4(kgate)) return fail(CA_ERR_INVALID, "gate_wk / kgate misaligned");
+    if (gate_heads != s.Hkv && gate_heads != s.Hq)
+        return fail(CA_ERR_INVALID, "gate_heads=%d must be num_kv_heads=%d or num_q_heads=%d", gate_heads, s.Hkv,
+                    s.Hq);
+    if ((rc = check_rope(rope_cos, rope_sin, rope_rows, max_nkb)) != CA_OK) return rc;
+    const ca::KvAddr none{};
+    hipError_t e = ca::launch_cache_fill(s, kn, kn, none, none, pb, nullptr, gate_wk, rope_cos, rope_sin, kgate,
+                                         pools, gate_heads / s.Hkv, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "gate_key_summaries launch");
+    return ok();
+}
+
+int ca_gate_query_summaries(const ca_dims* dims, const ca_seq_layout* q, const int32_t* past_blocks_host,
+                            int32_t pools, const float* gate_wq, int32_t gate_heads, const float* rope_cos,
+                            const float* rope_sin, int64_t rope_rows, float* qhat, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    ca::SeqAddr qa;
+    if ((rc = check_seq(q, "q", &qa)) != CA_OK) return rc;
+    if ((rc = check_pools(pools)) != CA_OK) return rc;
+    if (qhat == nullptr || !aligned4(qhat)) return fail(CA_ERR_INVALID, "qhat is NULL or misaligned");
+    const bool single = pools == CA_POOL_MAX || pools == CA_POOL_MIN || pools == CA_POOL_AVG;
+    if (gate_wq == nullptr) {
+        if (!single) return fail(CA_ERR_INVALID, "more than one query pool needs a projection (gate_wq)");
+        if (gate_heads != s.Hq)
+            return fail(CA_ERR_INVALID, "gate_heads=%d: unprojected query summaries have num_q_heads=%d heads",
+                        gate_heads, s.Hq);
+    } else {
+        if (!aligned4(gate_wq)) return fail(CA_ERR_INVALID, "gate_wq misaligned");
+        if (gate_heads != s.Hq && gate_heads != s.Hkv)
+            return fail(CA_ERR_INVALID, "gate_heads=%d must be num_q_heads=%d or num_kv_heads=%d", gate_heads, s.Hq,
+                        s.Hkv);
+    }
+    // the block RoPE applies with or without a projection (attn_gate.py:138-171)
+    if ((rc = check_rope(rope_cos, rope_sin, rope_rows, max_nkb)) != CA_OK) return rc;
+    const bool kv_aware = gate_wq != nullptr && gate_heads == s.Hkv && s.Hq != s.Hkv;
+    hipError_t e = ca::launch_pool_query(s, qa, pb, gate_wq, rope_cos, rope_sin, qhat, pools, kv_aware,
+                                         static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "gate_query_summaries launch");
     return ok();
 }
 
@@ -224,7 +295,7 @@ int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* pa
     if (qhat == nullptr) return fail(CA_ERR_INVALID, "qhat is NULL");
     if (gate_wq != nullptr && (rc = check_rope(rope_cos, rope_sin, rope_rows, max_nkb)) != CA_OK) return rc;
     hipError_t e = ca::launch_pool_query(s, qa, pb, gate_wq, gate_wq ? rope_cos : nullptr,
-                                         gate_wq ? rope_sin : nullptr, qhat,
+                                         gate_wq ? rope_sin : nullptr, qhat, CA_POOL_AVG, false,
                                          static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "pool_query launch");
     return ok();

@@ -248,8 +248,8 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int kv_tokens = qpos0 + s.Lq;
     auto issue_block = [&](int e, int stage) {
         const int kb = block_id(e);
-        const int64_t kphys = kpt ? sload(kpt + kb) : kb;
-        const int64_t vphys = vpt ? sload(vpt + kb) : kb;
+        const int64_t kphys = kpt ? clamp_page(sload(kpt + kb), p.k.max_page) : kb;
+        const int64_t vphys = vpt ? clamp_page(sload(vpt + kb), p.v.max_page) : kb;
         const int rows = min(kv_tokens - kb * 64, 64);
         const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
             const_cast<uint16_t*>(kbase_row + kphys * p.k.sblk), 0, rows * kstok_b, 0x00020000);
@@ -627,8 +627,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams 
     // flight while step st is computed.  One step is 8 K loads + 8 V DMA loads per wave.
     u32x4_t kf[2][2][4];
     uint8_t* vhalf[2] = {vbuf, vbuf + kDecVBytes / 2};
-    auto block_rsrc = [&](const uint16_t* base, const int32_t* pt, int64_t sblk, int kb, int stok_b) {
-        const int64_t phys = pt ? sload(pt + kb) : kb;
+    auto block_rsrc = [&](const uint16_t* base, const int32_t* pt, int32_t max_page, int64_t sblk, int kb,
+                          int stok_b) {
+        const int64_t phys = pt ? clamp_page(sload(pt + kb), max_page) : kb;
         const int rows = min(kv_tokens - kb * 64, 64);
         return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base + phys * sblk), 0, rows * stok_b,
                                                  0x00020000);
@@ -639,8 +640,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams 
     auto issue = [&](int st, int set) {
         const int kb = step_block(st);
         const int half = st & 1;
-        const __amdgpu_buffer_rsrc_t rk = block_rsrc(kbase_row, kpt, p.k.sblk, kb, kstok_b);
-        const __amdgpu_buffer_rsrc_t rv = block_rsrc(vbase_row, vpt, p.v.sblk, kb, vstok_b);
+        const __amdgpu_buffer_rsrc_t rk = block_rsrc(kbase_row, kpt, p.k.max_page, p.k.sblk, kb, kstok_b);
+        const __amdgpu_buffer_rsrc_t rv = block_rsrc(vbase_row, vpt, p.v.max_page, p.v.sblk, kb, vstok_b);
         const int kh = 32 * half * kstok_b;
         const int vh = 32 * half * vstok_b;
 #pragma unroll

@@ -18,7 +18,14 @@ struct KvAddr {
     int64_t sb, sh, sblk, stok;
     const int32_t* page_table;
     int64_t pts;
+    int32_t max_page;  // pages in the pool - 1 (page ids read from the table are clamped to it)
 };
+
+// Physical page of logical block kb of a row: the page table entry clamped into the pool, or
+// kb itself without a page table (a corrupt table cannot address outside the pool).
+__device__ __forceinline__ int64_t clamp_page(int32_t id, int32_t max_page) {
+    return id < 0 ? 0 : (id > max_page ? max_page : id);
+}
 
 struct SeqAddr {
     uint16_t* data;
@@ -29,14 +36,16 @@ struct Shape {
     int B, Lq, Hq, Hkv, G, Qb, cap, words;
 };
 
+// pools: CA_POOL_* set of the gate-K summary; gk: gate heads per KV head (1 or G)
 hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr& v_new,
                              const KvAddr& k_cache, const KvAddr& v_cache, const PastBlocks& pb,
                              float* kmean, const float* wk, const float* rope_cos,
-                             const float* rope_sin, float* kgate, hipStream_t stream);
+                             const float* rope_sin, float* kgate, int pools, int gk, hipStream_t stream);
 
+// pools: CA_POOL_* set; kv_aware: one output per KV head from its G heads' pooled vectors
 hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks& pb, const float* wq,
-                             const float* rope_cos, const float* rope_sin, float* qhat,
-                             hipStream_t stream);
+                             const float* rope_cos, const float* rope_sin, float* qhat, int pools,
+                             bool kv_aware, hipStream_t stream);
 
 // LDS bytes the score/select kernel needs for this shape (0 if unsupported).
 size_t score_select_lds_bytes(const Shape& s, bool compute);

@@ -24,14 +24,18 @@ namespace ca {
 namespace {
 
 // ---------------------------------------------------------------------------------------
-// Gate projection (per-head 128x128, y[o] = sum_i x[i] W[i][o], sequential fma over i) and
-// block RoPE y[i] = x[i] cos[i] + rotate_half(x)[i] sin[i].  64 threads; thread t owns the
-// output pair (t, t + 64), which is exactly a rotate_half pair.
-__device__ void gate_project_rope(const float* xs, const float* w, const float* rope_cos,
-                                  const float* rope_sin, int64_t pos, float* out) {
-    const int t = threadIdx.x;
+// Gate projection (per head [in, 128], y[o] = sum_i x[i] W[i][o], sequential fma over
+// i = 0 .. in-1) and block RoPE y[i] = x[i] cos[i] + rotate_half(x)[i] sin[i].  64 threads
+// (t = 0..63); thread t owns the output pair (t, t + 64), which is exactly a rotate_half pair.
+// Without w the input (in = 128) is rotated as it is.
+__device__ void gate_project_rope(const float* xs, int in, const float* w, const float* rope_cos,
+                                  const float* rope_sin, int64_t pos, float* out, int t) {
     float a0 = 0.0f, a1 = 0.0f;
-    for (int i = 0; i < kD; ++i) {
+    if (w == nullptr) {
+        a0 = xs[t];
+        a1 = xs[t + 64];
+    }
+    for (int i = 0; w != nullptr && i < in; ++i) {
         const float x = xs[i];
         a0 = __builtin_fmaf(x, w[i * kD + t], a0);
         a1 = __builtin_fmaf(x, w[i * kD + t + 64], a1);
@@ -69,6 +73,28 @@ __device__ __forceinline__ float block_mean_from_lds(const uint16_t* tile, int d
     return sum * 0.015625f;
 }
 
+// AttnGate pooling of head dim d over the 64 staged tokens (attn_gate.py:113-130,233-237):
+// the selected pools in the order max, min, avg go to xs[c*128 + d], c = 0, 1, ...  max and
+// min are strict compares from token 0 (bf16 values, exact); avg is block_mean_from_lds.
+__device__ __forceinline__ void block_pool_from_lds(const uint16_t* tile, int d, int pools, float* xs) {
+    float mx = bf16_to_f32(tile[d]), mn = mx, sum = 0.0f;
+#pragma unroll 16
+    for (int t = 0; t < kBlock; ++t) {
+        const float v = bf16_to_f32(tile[t * kTilePitch + d]);
+        mx = v > mx ? v : mx;
+        mn = v < mn ? v : mn;
+        sum = sum + v;
+    }
+    int c = 0;
+    if (pools & CA_POOL_MAX) xs[kD * c++ + d] = mx;
+    if (pools & CA_POOL_MIN) xs[kD * c++ + d] = mn;
+    if (pools & CA_POOL_AVG) xs[kD * c++ + d] = sum * 0.015625f;
+}
+
+__device__ __forceinline__ int pool_count(int pools) {
+    return (pools & 1) + ((pools >> 1) & 1) + ((pools >> 2) & 1);
+}
+
 typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 
 // Cache fill: one (new block, request x KV head) per workgroup.
@@ -76,9 +102,10 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
                                                          KvAddr kc, KvAddr vc, PastBlocks pb,
                                                          float* kmean, const float* wk,
                                                          const float* rope_cos,
-                                                         const float* rope_sin, float* kgate) {
+                                                         const float* rope_sin, float* kgate, int pools,
+                                                         int gk) {
     __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
-    __shared__ float xs[kD];
+    __shared__ float xs[3 * kD];
     const int j = blockIdx.x;
     const int row = blockIdx.y;
     const int b = row / s.Hkv;
@@ -92,8 +119,8 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
 #pragma unroll
     for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const u32x4_v*>(ks + (int64_t)(tok0 + 16 * i) * kn.st);
     if (kc.data != nullptr) {  // append K and V (summaries-only calls pass no cache)
-        const int64_t kphys = kc.page_table ? kc.page_table[(int64_t)row * kc.pts + kb] : kb;
-        const int64_t vphys = vc.page_table ? vc.page_table[(int64_t)row * vc.pts + kb] : kb;
+        const int64_t kphys = kc.page_table ? clamp_page(kc.page_table[(int64_t)row * kc.pts + kb], kc.max_page) : kb;
+        const int64_t vphys = vc.page_table ? clamp_page(vc.page_table[(int64_t)row * vc.pts + kb], vc.max_page) : kb;
         const uint16_t* vsrc = vn.data + b * vn.sb + (int64_t)j * kBlock * vn.st + hk * vn.sh + 8 * ch;
         uint16_t* kd = kc.data + b * kc.sb + hk * kc.sh + kphys * kc.sblk + 8 * ch;
         uint16_t* vd = vc.data + b * vc.sb + hk * vc.sh + vphys * vc.sblk + 8 * ch;
@@ -111,51 +138,68 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
     for (int i = 0; i < 4; ++i) *reinterpret_cast<u32x4_v*>(tile + (tok0 + 16 * i) * kTilePitch + 8 * ch) = kr[i];
     if (kmean == nullptr && wk == nullptr) return;
     __syncthreads();
-    const int64_t srow = ((int64_t)row * s.cap + kb) * kD;
     if (t < kD) {
-        const float m = block_mean_from_lds(tile, t);
-        if (kmean) kmean[srow + t] = m;
-        xs[t] = m;
+        if (kmean) kmean[((int64_t)row * s.cap + kb) * kD + t] = block_mean_from_lds(tile, t);
+        if (wk) block_pool_from_lds(tile, t, pools, xs);
     }
     if (wk == nullptr) return;
     __syncthreads();
-    if (t < 64) gate_project_rope(xs, wk + (int64_t)hk * kD * kD, rope_cos, rope_sin, kb, kgate + srow);
+    // gk gate heads per KV head: 1 (W_k per KV head) or G (the K block repeated to the Q heads
+    // hk*G + j and projected per Q head, attn_gate.py:30-33,84-86); four heads at a time
+    const int in = kD * pool_count(pools);
+    for (int jh = t >> 6; jh < gk; jh += 4) {
+        const int64_t gh = (int64_t)row * gk + jh;  // gate-head row (b*Hkv + hk)*gk + jh
+        gate_project_rope(xs, in, wk + (int64_t)(hk * gk + jh) * in * kD, rope_cos, rope_sin, kb,
+                          kgate + (gh * s.cap + kb) * kD, t & 63);
+    }
 }
 
 // ---------------------------------------------------------------------------------------
-// Query-block means (optionally gate-projected and rotated): one (block, request x head)
-// per workgroup.
+// Query-block summaries: the AttnGate pools (or the FlashPrefill mean) of one 64-token block,
+// optionally gate-projected and rotated.  One (block, request x head) per workgroup; with
+// kv_aware one (block, request x KV head) per workgroup, whose G heads' pooled vectors are
+// concatenated (g-major) before a per-KV-head projection (kv_group_aware_query,
+// attn_gate.py:74-79,96-113).
+constexpr int kMaxGateIn = 16 * 3 * kD;  // G <= 16 heads x 3 pools x 128
+
 __global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, PastBlocks pb,
                                                          const float* wq, const float* rope_cos,
-                                                         const float* rope_sin, float* qhat) {
+                                                         const float* rope_sin, float* qhat, int pools,
+                                                         int kv_aware) {
     __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
-    __shared__ float xs[kD];
+    __shared__ float xs[kMaxGateIn];
     const int qb = blockIdx.x;
     const int bh = blockIdx.y;
-    const int b = bh / s.Hq;
-    const int h = bh - b * s.Hq;
+    const int heads = kv_aware ? s.Hkv : s.Hq;
+    const int b = bh / heads;
+    const int h = bh - b * heads;
     const int t = threadIdx.x;
     const int tok0 = t >> 4;
     const int ch = t & 15;
-    const uint16_t* sp = q.data + b * q.sb + (int64_t)qb * kBlock * q.st + h * q.sh + 8 * ch;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int tok = tok0 + 16 * i;
-        *reinterpret_cast<u32x4_v*>(tile + tok * kTilePitch + 8 * ch) =
-            *reinterpret_cast<const u32x4_v*>(sp + (int64_t)tok * q.st);
-    }
-    __syncthreads();
+    const int C = pool_count(pools);
+    const int nsrc = kv_aware ? s.G : 1;
     float* out = qhat + ((int64_t)bh * s.Qb + qb) * kD;
-    if (t < kD) {
-        const float m = block_mean_from_lds(tile, t);
-        if (wq == nullptr)
-            out[t] = m;
-        else
-            xs[t] = m;
+    for (int g = 0; g < nsrc; ++g) {
+        const int hq = kv_aware ? h * s.G + g : h;
+        const uint16_t* sp = q.data + b * q.sb + (int64_t)qb * kBlock * q.st + hq * q.sh + 8 * ch;
+        if (g > 0) __syncthreads();  // the previous head's pooling is done with the tile
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int tok = tok0 + 16 * i;
+            *reinterpret_cast<u32x4_v*>(tile + tok * kTilePitch + 8 * ch) =
+                *reinterpret_cast<const u32x4_v*>(sp + (int64_t)tok * q.st);
+        }
+        __syncthreads();
+        if (t < kD) {
+            block_pool_from_lds(tile, t, pools, xs + g * C * kD);
+            if (wq == nullptr && rope_cos == nullptr) out[t] = xs[t];  // one pool, no projection, no RoPE
+        }
     }
-    if (wq == nullptr) return;
+    if (wq == nullptr && rope_cos == nullptr) return;
     __syncthreads();
-    if (t < 64) gate_project_rope(xs, wq + (int64_t)h * kD * kD, rope_cos, rope_sin, (int64_t)pb.p[b] + qb, out);
+    const int in = nsrc * C * kD;
+    const float* w = wq != nullptr ? wq + (int64_t)h * in * kD : nullptr;
+    if (t < 64) gate_project_rope(xs, in, w, rope_cos, rope_sin, (int64_t)pb.p[b] + qb, out, t);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -808,19 +852,19 @@ __global__ __launch_bounds__(kCsrThreads) void table_csr_kernel(CsrParams p) {
 hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr& v_new,
                              const KvAddr& k_cache, const KvAddr& v_cache, const PastBlocks& pb,
                              float* kmean, const float* wk, const float* rope_cos,
-                             const float* rope_sin, float* kgate, hipStream_t stream) {
+                             const float* rope_sin, float* kgate, int pools, int gk, hipStream_t stream) {
     dim3 grid(s.Qb, s.B * s.Hkv);
     hipLaunchKernelGGL(cache_fill_kernel, grid, dim3(256), 0, stream, s, k_new, v_new, k_cache,
-                       v_cache, pb, kmean, wk, rope_cos, rope_sin, kgate);
+                       v_cache, pb, kmean, wk, rope_cos, rope_sin, kgate, pools, gk);
     return hipGetLastError();
 }
 
 hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks& pb, const float* wq,
-                             const float* rope_cos, const float* rope_sin, float* qhat,
-                             hipStream_t stream) {
-    dim3 grid(s.Qb, s.B * s.Hq);
+                             const float* rope_cos, const float* rope_sin, float* qhat, int pools,
+                             bool kv_aware, hipStream_t stream) {
+    dim3 grid(s.Qb, s.B * (kv_aware ? s.Hkv : s.Hq));
     hipLaunchKernelGGL(pool_query_kernel, grid, dim3(256), 0, stream, s, q, pb, wq, rope_cos,
-                       rope_sin, qhat);
+                       rope_sin, qhat, pools, kv_aware ? 1 : 0);
     return hipGetLastError();
 }
 

@@ -1,23 +1,34 @@
-"""Paged KV cache owned by the compactattn path.
+"""Paged KV cache owned by the compactattn path: a page pool, a page table and an allocator.
 
 Replaces transformers' DynamicCache concatenation for the chunked-prefill layers
 (compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:518-536 and the
-heads-first _hf cache, modeling_llama_seerattn_chunked_dense_hf.py:59-82) plus the per-layer
-mean-K cache of the FlashPrefill model (modeling_llama_flashprefill_compactattn.py:121-150)
-and the gate K-block cache of the Seer model (modeling_llama_seerattn_chunked_dense.py:
-398-478).
+heads-first _hf cache, modeling_llama_seerattn_chunked_dense_hf.py:59-82), the grow-only page
+workspaces of the reference's paged prefill (compact_attn/kernels/varlen/
+indexed_dense_prefill_varlen.py:190-463), the per-layer mean-K cache of the FlashPrefill
+model (modeling_llama_flashprefill_compactattn.py:121-150) and the gate K-block cache of the
+Seer model (modeling_llama_seerattn_chunked_dense.py:398-478).
 
-Layout (one layer): K and V are heads-first [B, Hkv, cap*64, 128] bf16, i.e. 64-token
-pages with page id (b*Hkv + h)*cap + kb -- exactly the k_hf/v_hf view the reference's
-zero-copy path reads.  Block summaries are fp32 [B, Hkv, cap, 128]: kmean (FlashPrefill
-scoring) and, when a gate is attached, kgate (projected + rotated mean-K of the AttnGate).
-Appends go through the cache-fill kernel, which writes the chunk's pages and its
-summaries in one pass; nothing is ever re-copied.
+Layout of one layer:
+  - K and V pages: a pool of 64-token pages ``[num_pages, 64, 128]`` bf16 each (one 16 KiB
+    page per (request, KV head, logical block)); the pool only grows, and growing keeps every
+    page id (the contents move to the larger pool once);
+  - the page table: int32 ``[B*Hkv, blocks]`` (row = b*Hkv + h), logical block -> page id,
+    kept on the device for the kernels and mirrored on the host, where pages are allocated;
+  - block summaries by logical block: kmean ``[B, Hkv, blocks, 128]`` fp32 (FlashPrefill
+    scoring) and, with a gate, kgate ``[B, gate_heads, blocks, 128]`` fp32.
+Pages are reference-counted: ``fork`` lets a request share another's pages, and a decode
+append into a shared, partly filled page copies it first.  Appends write the chunk's pages
+and summaries in place through the cache-fill kernel; nothing is ever re-copied.
+
+Host-side allocation happens in ``append``/``append_tokens`` before the kernels are launched
+(a small page-table upload on the current stream), so a HIP graph that captures the chunk
+step must be recorded after the cache holds its pages (``reserve``).
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple
+from typing import List, Optional, Tuple
 
+import numpy as np
 import torch
 
 from . import ops
@@ -26,34 +37,161 @@ BLOCK = 64
 HEAD_DIM = 128
 
 
+class PagePool:
+    """Grow-only pool of 64-token K and V pages with reference counts."""
+
+    def __init__(self, num_pages: int, device):
+        num_pages = max(int(num_pages), 1)
+        self.device = torch.device(device)
+        self.k = torch.zeros((num_pages, BLOCK, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+        self.v = torch.zeros_like(self.k)
+        self.refs = np.zeros(num_pages, np.int32)
+        self._free: List[int] = list(range(num_pages - 1, -1, -1))  # pop() hands out ascending ids
+
+    @property
+    def num_pages(self) -> int:
+        return self.k.shape[0]
+
+    @property
+    def free_pages(self) -> int:
+        return len(self._free)
+
+    def alloc(self, n: int) -> List[int]:
+        """n fresh pages (reference count 1); the pool grows (at least doubling) when short."""
+        if n > len(self._free):
+            self._grow(n - len(self._free))
+        pages = [self._free.pop() for _ in range(n)]
+        self.refs[pages] = 1
+        return pages
+
+    def retain(self, pages) -> None:
+        np.add.at(self.refs, np.asarray(pages, np.int64), 1)
+
+    def release(self, pages) -> None:
+        for p in np.asarray(pages, np.int64).ravel().tolist():
+            if self.refs[p] <= 0:
+                raise RuntimeError(f"page {p} released more often than it was taken")
+            self.refs[p] -= 1
+            if self.refs[p] == 0:
+                self._free.append(p)
+
+    def _grow(self, need: int) -> None:
+        old = self.num_pages
+        new = max(2 * old, old + need)
+        for name in ("k", "v"):
+            t = torch.zeros((new, BLOCK, HEAD_DIM), dtype=torch.bfloat16, device=self.device)
+            t[:old].copy_(getattr(self, name))
+            setattr(self, name, t)
+        self.refs = np.concatenate([self.refs, np.zeros(new - old, np.int32)])
+        self._free = list(range(new - 1, old - 1, -1)) + self._free
+
+
 class PagedKVCache:
+    """One layer's paged K/V cache for ``batch`` requests that advance together."""
+
     def __init__(self, batch: int, num_kv_heads: int, max_tokens: int, device, with_kmean: bool = True,
-                 with_kgate: bool = False):
-        if max_tokens % BLOCK:
-            raise ValueError("max_tokens must be a multiple of 64")
+                 with_kgate: bool = False, kgate_heads: Optional[int] = None, pool_pages: Optional[int] = None):
+        """max_tokens sizes the page table and summaries (they grow on demand); pool_pages
+        sizes the initial page pool (default: every row's max_tokens)."""
         self.batch = batch
         self.num_kv_heads = num_kv_heads
-        self.cap = max_tokens // BLOCK
+        self.rows = batch * num_kv_heads
         self.device = torch.device(device)
-        self.k = torch.zeros((batch, num_kv_heads, self.cap * BLOCK, HEAD_DIM), dtype=torch.bfloat16, device=device)
-        self.v = torch.zeros_like(self.k)
-        self.kmean = (torch.zeros((batch, num_kv_heads, self.cap, HEAD_DIM), dtype=torch.float32, device=device)
-                      if with_kmean else None)
-        self.kgate = (torch.zeros((batch, num_kv_heads, self.cap, HEAD_DIM), dtype=torch.float32, device=device)
-                      if with_kgate else None)
-        self.length = 0  # tokens stored per request (all requests advance together)
+        self.cap = max(-(-int(max_tokens) // BLOCK), 1)  # blocks per row of the table and summaries
+        self.pool = PagePool(pool_pages if pool_pages is not None else self.rows * self.cap, self.device)
+        self._pt = np.full((self.rows, self.cap), -1, np.int32)  # host mirror; -1 = unmapped
+        self.page_table = torch.full((self.rows, self.cap), -1, dtype=torch.int32, device=self.device)
+        self.kgate_heads = kgate_heads or num_kv_heads
+        self.kmean = self._summary(num_kv_heads) if with_kmean else None
+        self.kgate = self._summary(self.kgate_heads) if with_kgate else None
+        self.length = 0  # tokens stored per request
+
+    # -- layout ---------------------------------------------------------------------------
+    def _summary(self, heads: int) -> torch.Tensor:
+        return torch.zeros((self.batch, heads, self.cap, HEAD_DIM), dtype=torch.float32, device=self.device)
 
     @property
     def past_blocks(self) -> int:
         return self.length // BLOCK
 
     def layouts(self) -> Tuple[ops.KV, ops.KV]:
-        return ops.KV.heads_first(self.k), ops.KV.heads_first(self.v)
+        """K and V as (pool, page table) layouts for the kernels."""
+        return ops.KV.paged(self.pool.k, self.page_table), ops.KV.paged(self.pool.v, self.page_table)
 
+    def pages_of(self, b: int, h: int) -> List[int]:
+        """Page ids of request b, KV head h, in logical block order (the mapped blocks)."""
+        row = self._pt[b * self.num_kv_heads + h]
+        return row[row >= 0].tolist()
+
+    # -- allocation -----------------------------------------------------------------------
+    def _grow_cap(self, blocks: int) -> None:
+        if blocks <= self.cap:
+            return
+        new = max(2 * self.cap, blocks)
+        pt = np.full((self.rows, new), -1, np.int32)
+        pt[:, :self.cap] = self._pt
+        self._pt = pt
+        dev_pt = torch.full((self.rows, new), -1, dtype=torch.int32, device=self.device)
+        dev_pt[:, :self.cap].copy_(self.page_table)
+        self.page_table = dev_pt
+        for name in ("kmean", "kgate"):
+            old = getattr(self, name)
+            if old is not None:
+                t = torch.zeros((old.shape[0], old.shape[1], new, HEAD_DIM), dtype=torch.float32, device=self.device)
+                t[:, :, :self.cap].copy_(old)
+                setattr(self, name, t)
+        self.cap = new
+
+    def _upload(self, b0: int, b1: int) -> None:
+        if b1 > b0:
+            self.page_table[:, b0:b1].copy_(torch.from_numpy(np.ascontiguousarray(self._pt[:, b0:b1])))
+
+    def _map(self, b0: int, b1: int) -> None:
+        """Give every row a page for each unmapped logical block in [b0, b1)."""
+        self._grow_cap(b1)
+        need = self._pt[:, b0:b1] < 0
+        n = int(need.sum())
+        if n:
+            pages = np.asarray(self.pool.alloc(n), np.int32)
+            block = self._pt[:, b0:b1]
+            block[need] = pages  # row-major: a row's new blocks get ascending page ids
+            self._pt[:, b0:b1] = block
+        self._upload(b0, b1)
+
+    def reserve(self, tokens: int) -> None:
+        """Map pages for the first ``tokens`` tokens of every request ahead of time."""
+        self._map(0, -(-int(tokens) // BLOCK))
+
+    def _unshare(self, kb: int) -> None:
+        """Copy-on-write of logical block kb: rows (in order) whose page still has other holders
+        move to a copy; the last holder of a page keeps it."""
+        col = self._pt[:, kb]
+        refs = {int(p): int(self.pool.refs[p]) for p in col if p >= 0}
+        moved = []
+        for r in range(self.rows):
+            p = int(col[r])
+            if p >= 0 and refs[p] > 1:
+                refs[p] -= 1
+                moved.append(r)
+        if not moved:
+            return
+        old = [int(col[r]) for r in moved]
+        fresh = self.pool.alloc(len(moved))
+        src = torch.as_tensor(old, device=self.device, dtype=torch.long)
+        dst = torch.as_tensor(fresh, device=self.device, dtype=torch.long)
+        self.pool.k[dst] = self.pool.k[src]
+        self.pool.v[dst] = self.pool.v[src]
+        self.pool.release(old)
+        for r, p in zip(moved, fresh):
+            self._pt[r, kb] = p
+        self._upload(kb, kb + 1)
+
+    # -- appends --------------------------------------------------------------------------
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, gate_wk: Optional[torch.Tensor] = None,
                rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None) -> int:
-        """Append [B, L, Hkv, 128] bf16 K/V (L a multiple of 64); returns the number of past
-        blocks before the append."""
+        """Append [B, L, Hkv, 128] bf16 K/V (L a multiple of 64) through the cache-fill kernel,
+        which also writes the new blocks' kmean (and, with gate_wk [Hkv, 128, 128], the
+        avg-pooled gate-K summaries); returns the number of past blocks before the append."""
         B, L, Hkv, _ = k_new.shape
         if B != self.batch or Hkv != self.num_kv_heads:
             raise ValueError("k_new does not match the cache's batch / KV heads")
@@ -61,11 +199,10 @@ class PagedKVCache:
             raise ValueError("appended chunks must be multiples of 64 tokens")
         if self.length % BLOCK:
             raise ValueError("chunked prefill cannot follow decode steps that left a partial block")
-        if self.length + L > self.cap * BLOCK:
-            raise ValueError(f"cache capacity {self.cap * BLOCK} tokens exceeded")
-        if gate_wk is not None and self.kgate is None:
-            raise ValueError("cache built without a gate-K summary buffer")
+        if gate_wk is not None and (self.kgate is None or self.kgate_heads != Hkv):
+            raise ValueError("cache built without a per-KV-head gate-K summary buffer")
         past = self.past_blocks
+        self._map(past, past + L // BLOCK)
         K, V = self.layouts()
         ops.cache_fill(k_new, v_new, K, V, [past] * B, self.cap, self.kmean, gate_wk=gate_wk, rope_cos=rope_cos,
                        rope_sin=rope_sin, kgate=self.kgate if gate_wk is not None else None)
@@ -80,19 +217,62 @@ class PagedKVCache:
         B, L, Hkv, _ = k_new.shape
         if B != self.batch or Hkv != self.num_kv_heads:
             raise ValueError("k_new does not match the cache's batch / KV heads")
-        if self.length + L > self.cap * BLOCK:
-            raise ValueError(f"cache capacity {self.cap * BLOCK} tokens exceeded")
+        if L == 0:
+            return self.length
         start = self.length
-        self.k[:, :, start:start + L].copy_(k_new.transpose(1, 2))
-        self.v[:, :, start:start + L].copy_(v_new.transpose(1, 2))
-        self.length += L
+        end = start + L
+        self._map(start // BLOCK, -(-end // BLOCK))
+        if start % BLOCK:
+            self._unshare(start // BLOCK)
+        pos = np.arange(start, end)
+        pages = self._pt[:, pos // BLOCK].astype(np.int64)  # [rows, L]
+        flat = torch.from_numpy(pages * BLOCK + (pos % BLOCK)[None, :]).to(self.device)
+        kf = self.pool.k.view(-1, HEAD_DIM)
+        vf = self.pool.v.view(-1, HEAD_DIM)
+        kf[flat.reshape(-1)] = k_new.transpose(1, 2).reshape(-1, HEAD_DIM)
+        vf[flat.reshape(-1)] = v_new.transpose(1, 2).reshape(-1, HEAD_DIM)
+        self.length = end
         return start
 
+    # -- sharing --------------------------------------------------------------------------
+    def fork(self, src: int, dst: int) -> None:
+        """Request dst takes request src's contents by sharing its pages (no copy): dst's own
+        pages are released, src's gain a reference, and the summaries of src are copied."""
+        if src == dst:
+            return
+        nb = -(-self.length // BLOCK)
+        H = self.num_kv_heads
+        for h in range(H):
+            rs, rd = src * H + h, dst * H + h
+            old = self._pt[rd][self._pt[rd] >= 0]
+            self.pool.release(old)
+            self._pt[rd] = -1
+            self._pt[rd, :nb] = self._pt[rs, :nb]
+            self.pool.retain(self._pt[rs, :nb])
+        self._upload(0, self.cap)
+        for t in (self.kmean, self.kgate):
+            if t is not None:
+                t[dst].copy_(t[src])
+
+    # -- views ----------------------------------------------------------------------------
+    def _gather(self, pool: torch.Tensor) -> torch.Tensor:
+        nb = -(-self.length // BLOCK)
+        idx = torch.from_numpy(self._pt[:, :nb].astype(np.int64)).to(self.device)
+        pages = pool[idx.reshape(-1)].view(self.batch, self.num_kv_heads, nb * BLOCK, HEAD_DIM)
+        return pages[:, :, :self.length]
+
     def k_hf(self) -> torch.Tensor:
-        return self.k[:, :, :self.length]
+        """The stored keys as a heads-first [B, Hkv, length, 128] tensor (a gathered copy)."""
+        return self._gather(self.pool.k)
 
     def v_hf(self) -> torch.Tensor:
-        return self.v[:, :, :self.length]
+        return self._gather(self.pool.v)
 
     def reset(self) -> None:
+        """Drop every request's pages (the pool keeps its size)."""
+        mapped = self._pt[self._pt >= 0]
+        if mapped.size:
+            self.pool.release(mapped)
+        self._pt[:] = -1
+        self.page_table.fill_(-1)
         self.length = 0

@@ -65,10 +65,40 @@ def _rope_theta(hf_config) -> float:
     return float(theta)
 
 
+# The gate settings of the reference's SeerAttnLlamaConfig defaults
+# (compact_attn/prefill_sparse/llama/configuration_llama_seerattn.py:191,198,202), which apply
+# when the gate checkpoint's config.json does not set them.
+_GATE_DEFAULTS = {
+    "seerattn_gate_type": "Qavg_Kmaxminavg",
+    "seerattn_gate_force_double": False,
+    "seerattn_compactattn_kv_group_aware_gate": False,
+}
+
+
+def _gate_settings(model_id: Optional[str]) -> dict:
+    """Gate type / force_double / kv-group-aware flag from the gate checkpoint's config.json
+    (a local directory; plain JSON), else the reference's defaults -- the reference reads the
+    same fields through SeerAttnLlamaConfig.from_pretrained(model_id)
+    (compact_attn/load_attention_replacement.py:131-132)."""
+    import json
+
+    out = dict(_GATE_DEFAULTS)
+    if model_id is None or not os.path.isdir(model_id):
+        return out
+    path = os.path.join(model_id, "config.json")
+    if os.path.isfile(path):
+        with open(path) as f:
+            cfg = json.load(f)
+        for key in out:
+            if key in cfg:
+                out[key] = type(_GATE_DEFAULTS[key])(cfg[key])
+    return out
+
+
 def _build_seer_config(hf_config, *, variant: str, threshold: float, compactattn_keep_recent_blocks: int,
                        flashprefill_alpha: float, flashprefill_block_size: int, flashprefill_attention_sink: int,
                        flashprefill_window_size: int, flashprefill_last_n_block: int,
-                       flashprefill_min_budget: int) -> SeerAttnLlamaConfig:
+                       flashprefill_min_budget: int, gate: Optional[dict] = None) -> SeerAttnLlamaConfig:
     head_dim = getattr(hf_config, "head_dim", None) or hf_config.hidden_size // hf_config.num_attention_heads
     cfg = SeerAttnLlamaConfig(
         vocab_size=hf_config.vocab_size,
@@ -89,6 +119,7 @@ def _build_seer_config(hf_config, *, variant: str, threshold: float, compactattn
         seerattn_flashprefill_window_size=int(flashprefill_window_size),
         seerattn_flashprefill_last_n_block=int(flashprefill_last_n_block),
         seerattn_flashprefill_min_budget=int(flashprefill_min_budget),
+        **(gate or {}),
     )
     cfg.validate()
     return cfg
@@ -188,7 +219,7 @@ def load_llama_attention_replacement_model(
         compactattn_keep_recent_blocks=compactattn_keep_recent_blocks, flashprefill_alpha=flashprefill_alpha,
         flashprefill_block_size=flashprefill_block_size, flashprefill_attention_sink=flashprefill_attention_sink,
         flashprefill_window_size=flashprefill_window_size, flashprefill_last_n_block=flashprefill_last_n_block,
-        flashprefill_min_budget=flashprefill_min_budget)
+        flashprefill_min_budget=flashprefill_min_budget, gate=_gate_settings(model_id))
     block_rope = _BlockRope(model.model.rotary_emb, seer_cfg.max_position_embeddings)
     cls = _VARIANTS[variant]
     for layer_idx, layer in enumerate(model.model.layers):

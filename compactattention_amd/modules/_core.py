@@ -60,6 +60,34 @@ def geometry(query_states: torch.Tensor, kv_len: int, num_kv_heads: int, block_s
     return ChunkGeometry(bsz, q_len, kv_len, num_q_heads, num_kv_heads, P, Qb, P + Qb)
 
 
+def aligned_head(q_len: int, kv_len: int) -> Optional[int]:
+    """None for a block-aligned call (q_len and kv_len multiples of 64).  Otherwise the query
+    tokens of its block-aligned head: 0 when fewer than 64 queries (the whole call attends
+    densely), else q_len rounded down to 64 -- the head runs the selecting path over the first
+    kv_len - (q_len - head) keys and the last q_len % 64 queries attend densely to all kv_len
+    keys (dense_tail).  A chunk of 64 or more queries must start at a block boundary."""
+    if q_len % BLOCK == 0 and kv_len % BLOCK == 0:
+        return None
+    if kv_len < q_len:
+        raise ValueError(f"kv_len={kv_len} < q_len={q_len}")
+    if q_len < BLOCK:
+        return 0
+    if (kv_len - q_len) % BLOCK:
+        raise ValueError(f"a chunk of {q_len} queries over {kv_len} keys must start at a 64-token block boundary")
+    return q_len - q_len % BLOCK
+
+
+def dense_tail(query_states: torch.Tensor, K: ops.KV, V: ops.KV, kv_len: int, num_kv_heads: int,
+               softmax_scale: Optional[float]) -> torch.Tensor:
+    """Queries [B, n, Hq, 128] (n <= 64) at the last n of kv_len positions attend to every key
+    before them (bottom-right causal) through the decode kernel, which reads the partial last
+    block up to kv_len only -- the reference's dense fallback (flashprefill_prefill.py:903-907,
+    _dense_prefill_full_kv)."""
+    scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(HEAD_DIM)
+    B = query_states.shape[0]
+    return ops.attn_decode(query_states, K, V, [kv_len] * B, scale, -(-kv_len // BLOCK), num_kv_heads)
+
+
 def kv_layouts(key_states: Optional[torch.Tensor], value_states: Optional[torch.Tensor],
                k_hf: Optional[torch.Tensor], v_hf: Optional[torch.Tensor]) -> Tuple[ops.KV, ops.KV]:
     """Prefer the heads-first cache (zero copy, the reference's fi_zero_copy view); else read

@@ -12,9 +12,11 @@ last_n_block query blocks stay out of the union; the current chunk is always kep
 the GQA union, int32 block tables and the indexed attention.
 
 Scores are the pooled softmax of flash_prefill_score_chunked_from_mean_k (see
-compactattention_amd.flashprefill_vendor).  A first chunk (kv_len == q_len) or q_len <= 1
-runs dense causal attention on the same HIP kernel (identity tables), where the reference
-calls its dense backend.
+compactattention_amd.flashprefill_vendor).  A first chunk (kv_len == q_len) runs dense causal
+attention on the same HIP kernel (identity tables), and a call with fewer than 64 queries
+attends densely through the decode kernel, where the reference calls its dense backend
+(q_len <= 1 or kv_len <= q_len, :903-907).  A longer chunk whose length is not a multiple of
+64 selects for its block-aligned head and runs its last q_len % 64 queries densely.
 """
 from __future__ import annotations
 
@@ -25,8 +27,8 @@ import torch
 
 from .. import ops
 from ..flashprefill_vendor import mean_k_kernel_layout
-from ._core import (COMPACTATTN_VERSION, INDEXED_IMPLS, StageTimer, attend, check_attention_mask, dense_tables,
-                    geometry, kv_layouts, table_stats)
+from ._core import (COMPACTATTN_VERSION, INDEXED_IMPLS, StageTimer, aligned_head, attend, check_attention_mask,
+                    dense_tables, dense_tail, geometry, kv_layouts, table_stats)
 from .attention_forward_chunked_dense import CACHE_FILL_BACKENDS, PACK_IMPLS
 
 
@@ -68,6 +70,28 @@ def flashprefill_compactattn_prefill_full_kv(
         raise ValueError(f"Unsupported cache_fill_backend: {cache_fill_backend}")
     kv_len = k_hf.shape[2] if k_hf is not None else key_states.shape[1]
     num_kv_heads = k_hf.shape[1] if k_hf is not None else key_states.shape[2]
+    head = aligned_head(query_states.shape[1], kv_len) if block_size == 64 else None
+    if head is not None:
+        # fewer than 64 queries: dense over the whole KV (the reference's dense fallback for
+        # q_len <= 1, :903-907); otherwise the aligned head selects and the tail is dense
+        check_attention_mask(attention_mask, query_states.shape[0], kv_len)
+        K, V = kv_layouts(key_states, value_states, k_hf, v_hf)
+        stats: Dict[str, float] = {"compactattn_version": COMPACTATTN_VERSION}
+        parts = []
+        if head > 0:
+            keep = kv_len - (query_states.shape[1] - head)
+            cut = lambda t, dim: None if t is None else t.narrow(dim, 0, keep)  # noqa: E731
+            out_head, stats = flashprefill_compactattn_prefill_full_kv(
+                query_states[:, :head], cut(key_states, 1), cut(value_states, 1), cut(attention_mask, 1),
+                softmax_scale=softmax_scale, num_key_value_groups=num_key_value_groups, block_size=block_size,
+                attention_sink=attention_sink, window_size=window_size, alpha=alpha, last_n_block=last_n_block,
+                min_budget=min_budget, pack_impl=pack_impl, indexed_impl=indexed_impl,
+                cache_fill_backend=cache_fill_backend, measure_timing=measure_timing, k_hf=cut(k_hf, 2),
+                v_hf=cut(v_hf, 2), mean_k_cache=mean_k_cache)
+            parts.append(out_head)
+        parts.append(dense_tail(query_states[:, head:], K, V, kv_len, num_kv_heads, softmax_scale))
+        stats["flashprefill_dense_tail_tokens"] = float(query_states.shape[1] - head)
+        return torch.cat(parts, dim=1) if len(parts) > 1 else parts[0], stats
     geo = geometry(query_states, kv_len, num_kv_heads, block_size)
     if geo.group != num_key_value_groups:
         raise ValueError(f"num_key_value_groups={num_key_value_groups} does not match heads "
@@ -78,7 +102,7 @@ def flashprefill_compactattn_prefill_full_kv(
     P = [geo.past_blocks] * geo.batch
     stats: Dict[str, float] = {"compactattn_version": COMPACTATTN_VERSION}
 
-    if geo.q_len <= 1 or geo.past_blocks == 0:
+    if geo.past_blocks == 0:
         table, counts = dense_tables(geo, query_states.device)
         out = timer("attention_ms", lambda: attend(query_states, K, V, table, counts, geo, softmax_scale))
         stats["flashprefill_dense_calls"] = 1.0

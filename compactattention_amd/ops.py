@@ -14,7 +14,25 @@ from typing import Optional, Sequence, Tuple
 import torch
 
 from . import _hip
-from ._hip import BLOCK, HEAD_DIM, Dims, KvLayout, SelectRule, SeqLayout, check
+from ._hip import BLOCK, HEAD_DIM, POOL_AVG, POOL_MAX, POOL_MIN, Dims, KvLayout, SelectRule, SeqLayout, check
+
+POOL_BITS = {"max": POOL_MAX, "min": POOL_MIN, "avg": POOL_AVG}
+
+
+def pool_bits(names: Sequence[str]) -> int:
+    """Pool names ('max', 'min', 'avg') -> CA_POOL_* bits; the kernels concatenate the pooled
+    vectors in the order max, min, avg, the order of the reference's generated gate classes
+    (itertools.combinations over ['max', 'min', 'avg'], attn_gate.py:265-278)."""
+    out = 0
+    for nm in names:
+        if nm not in POOL_BITS:
+            raise ValueError(f"unknown pooling function {nm!r}")
+        out |= POOL_BITS[nm]
+    order = [nm for nm in ("max", "min", "avg") if nm in names]
+    if list(names) != order or not names:
+        raise ValueError(f"pooling functions {tuple(names)} must be a non-empty subset of ('max', 'min', 'avg') "
+                         "in that order")
+    return out
 
 
 @dataclass(frozen=True)
@@ -114,8 +132,8 @@ class KV:
         _need_cuda("kv", t, torch.bfloat16)
         if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
             raise ValueError("seq-first KV must be [B, K, Hkv, 128] with a contiguous last dim")
-        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(2), BLOCK * t.stride(1), t.stride(1), None, 0),
-                  tokens=t.shape[1])
+        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(2), BLOCK * t.stride(1), t.stride(1), None, 0,
+                              0), tokens=t.shape[1])
 
     @staticmethod
     def heads_first(t: torch.Tensor) -> "KV":
@@ -123,8 +141,8 @@ class KV:
         _need_cuda("kv", t, torch.bfloat16)
         if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
             raise ValueError("heads-first KV must be [B, Hkv, K, 128] with a contiguous last dim")
-        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(1), BLOCK * t.stride(2), t.stride(2), None, 0),
-                  tokens=t.shape[2])
+        return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(1), BLOCK * t.stride(2), t.stride(2), None, 0,
+                              0), tokens=t.shape[2])
 
     @staticmethod
     def paged(pool: torch.Tensor, page_table: torch.Tensor) -> "KV":
@@ -136,7 +154,20 @@ class KV:
         if page_table.dim() != 2 or page_table.stride(1) != 1:
             raise ValueError("page_table must be [rows, blocks] with contiguous rows")
         return KV(pool, KvLayout(pool.data_ptr(), 0, 0, pool.stride(0), pool.stride(1), page_table.data_ptr(),
-                                 page_table.stride(0)), page_table)
+                                 page_table.stride(0), pool.shape[0]), page_table)
+
+    def check_blocks(self, name: str, batch_rows: int, blocks: int, tokens: Optional[int] = None) -> None:
+        """Raise unless this layout covers ``blocks`` logical blocks of each of ``batch_rows``
+        rows: page-table columns, or for a contiguous cache whole 64-token blocks (``tokens``
+        tokens instead when the kernel's reads stop at that length)."""
+        need = BLOCK * blocks if tokens is None else tokens
+        if self.tokens is not None and self.tokens < need:
+            raise ValueError(f"{name} cache holds {self.tokens} tokens; the call addresses {blocks} blocks "
+                             f"({need} tokens)")
+        if self.page_table is not None:
+            if self.page_table.shape[0] < batch_rows or self.page_table.shape[1] < blocks:
+                raise ValueError(f"{name} page_table {tuple(self.page_table.shape)} does not cover "
+                                 f"[{batch_rows}, {blocks}]")
 
 
 def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Optional[KV], v_cache: Optional[KV],
@@ -152,6 +183,12 @@ def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Opti
     if (k_cache is None) != (v_cache is None):
         raise ValueError("k_cache and v_cache must both be given or both be None")
     vn = seq_layout(v_new, "v_new") if k_cache is not None else None
+    if vn is not None and tuple(v_new.shape) != tuple(k_new.shape):
+        raise ValueError("v_new must have k_new's shape")
+    blocks = max(int(p) for p in past_blocks) + Lq // BLOCK  # highest block written + 1
+    for name, kv in (("k", k_cache), ("v", v_cache)):
+        if kv is not None:
+            kv.check_blocks(name, B * Hkv, blocks)
     if kmean is not None:
         _need_cuda("kmean", kmean, torch.float32)
         if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
@@ -164,6 +201,8 @@ def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Opti
         if kgate is None:
             raise ValueError("kgate output is required with gate_wk")
         _need_cuda("kgate", kgate, torch.float32)
+        if not kgate.is_contiguous() or kgate.numel() < B * Hkv * kv_cap * HEAD_DIM:
+            raise ValueError("kgate must be contiguous [B*Hkv, kv_cap, 128] fp32")
         if rope_cos is not None:
             _need_cuda("rope_cos", rope_cos, torch.float32)
             _need_cuda("rope_sin", rope_sin, torch.float32)
@@ -194,6 +233,76 @@ def pool_query(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, gate_wq
     qhat = torch.empty((B, Hq, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
     check(_hip.lib().ca_pool_query(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks), _ptr(gate_wq),
                                    _ptr(rope_cos), _ptr(rope_sin), rope_rows, qhat.data_ptr(), _stream()))
+    return qhat
+
+
+def _rope_args(rope_cos: Optional[torch.Tensor], rope_sin: Optional[torch.Tensor]) -> int:
+    if (rope_cos is None) != (rope_sin is None):
+        raise ValueError("rope_cos and rope_sin must both be given or both be None")
+    if rope_cos is None:
+        return 0
+    for name, t in (("rope_cos", rope_cos), ("rope_sin", rope_sin)):
+        _need_cuda(name, t, torch.float32)
+        if t.dim() != 2 or t.shape[1] != HEAD_DIM or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous fp32 [rows, {HEAD_DIM}]")
+    return rope_cos.shape[0]
+
+
+def pool_count(pools: int) -> int:
+    return bin(int(pools) & 7).count("1")
+
+
+def gate_key_summaries(k_new: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, pools: int,
+                       gate_wk: torch.Tensor, kgate: torch.Tensor, num_q_heads: Optional[int] = None,
+                       rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None) -> None:
+    """AttnGate K summaries of the chunk's blocks: pools (POOL_* bits, concatenated max, min,
+    avg) -> per-head projection gate_wk [gate_heads, C*128, 128] -> block RoPE, written into
+    kgate [B, gate_heads, kv_cap, 128] at blocks past_blocks[b]...  gate_heads is Hkv or the
+    number of Q heads (the K block repeated to each Q head of its group)."""
+    B, Lq, Hkv, _ = k_new.shape
+    Hq = num_q_heads or Hkv
+    kn = seq_layout(k_new, "k_new")
+    _need_cuda("gate_wk", gate_wk, torch.float32)
+    _need_cuda("kgate", kgate, torch.float32)
+    gh = gate_wk.shape[0]
+    if gate_wk.dim() != 3 or tuple(gate_wk.shape[1:]) != (pool_count(pools) * HEAD_DIM, HEAD_DIM) \
+            or not gate_wk.is_contiguous():
+        raise ValueError(f"gate_wk must be contiguous [heads, {pool_count(pools) * HEAD_DIM}, {HEAD_DIM}] fp32")
+    if not kgate.is_contiguous() or kgate.numel() < B * gh * kv_cap * HEAD_DIM:
+        raise ValueError(f"kgate must be contiguous [B, {gh}, kv_cap, 128] fp32")
+    rows = _rope_args(rope_cos, rope_sin)
+    d = make_dims(B, Lq, Hq, Hkv, kv_cap)
+    check(_hip.lib().ca_gate_key_summaries(ctypes.byref(d), ctypes.byref(kn), past_array(past_blocks), int(pools),
+                                           gate_wk.data_ptr(), gh, _ptr(rope_cos), _ptr(rope_sin), rows,
+                                           kgate.data_ptr(), _stream()))
+
+
+def gate_query_summaries(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, pools: int,
+                         gate_wq: Optional[torch.Tensor], num_kv_heads: int,
+                         rope_cos: Optional[torch.Tensor] = None,
+                         rope_sin: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """AttnGate query summaries: [B, Lq, Hq, 128] bf16 -> [B, gate_heads, Lq/64, 128] fp32.
+    gate_wq None: one pool, no projection (gate_heads = Hq).  gate_wq [Hq, C*128, 128]: per
+    Q head.  gate_wq [Hkv, G*C*128, 128]: the kv-group-aware form (the group's G heads
+    pooled and concatenated head-major, one output per KV head)."""
+    B, Lq, Hq, _ = q.shape
+    ql = seq_layout(q, "q")
+    C = pool_count(pools)
+    G = Hq // num_kv_heads
+    if gate_wq is None:
+        gh = Hq
+    else:
+        _need_cuda("gate_wq", gate_wq, torch.float32)
+        gh = gate_wq.shape[0]
+        width = (G if (gh == num_kv_heads and G > 1) else 1) * C * HEAD_DIM
+        if gate_wq.dim() != 3 or tuple(gate_wq.shape[1:]) != (width, HEAD_DIM) or not gate_wq.is_contiguous():
+            raise ValueError(f"gate_wq must be contiguous [{gh}, {width}, {HEAD_DIM}] fp32")
+    rows = _rope_args(rope_cos, rope_sin)
+    d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
+    qhat = torch.empty((B, gh, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
+    check(_hip.lib().ca_gate_query_summaries(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks), int(pools),
+                                             _ptr(gate_wq), gh, _ptr(rope_cos), _ptr(rope_sin), rows, qhat.data_ptr(),
+                                             _stream()))
     return qhat
 
 
@@ -343,8 +452,13 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
     ol = seq_layout(out, "out")
     _need_cuda("table", table, torch.int32)
     _need_cuda("counts", counts, torch.int32)
-    if table.dim() != 2 or table.stride(1) != 1 or table.shape[0] < B * num_kv_heads:
+    if table.dim() != 2 or table.stride(1) != 1 or table.shape[0] < B * num_kv_heads or table.shape[1] < kv_cap:
         raise ValueError("table must be [B*Hkv, >= kv_cap] with contiguous rows")
+    if counts.numel() < B * num_kv_heads:
+        raise ValueError("counts must hold B*Hkv entries")
+    blocks = max(int(p) for p in past_blocks) + Lq // BLOCK  # blocks a row's table may name
+    for name, kv in (("k", k), ("v", v)):
+        kv.check_blocks(name, B * num_kv_heads, blocks)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     pa = past_array(past_blocks)
     # num_splits = 0 hands the choice to the library
@@ -386,10 +500,11 @@ def attn_decode(q: torch.Tensor, k: KV, v: KV, kv_len: Sequence[int], scale: flo
         out = torch.empty_like(q)
     ol = seq_layout(out, "out")
     # the kernel moves whole 64-token blocks: contiguous caches must hold the last one entirely
-    need_tok = BLOCK * ((max(int(x) for x in kv_len) + BLOCK - 1) // BLOCK)
+    # the kernel's buffer ranges end at each request's kv_len: a contiguous cache needs those
+    # tokens only, a paged one a page for every block they touch
+    max_len = max(int(x) for x in kv_len)
     for name, kv in (("k", k), ("v", v)):
-        if kv.tokens is not None and kv.tokens < need_tok:
-            raise ValueError(f"{name} cache holds {kv.tokens} tokens; decode reads whole blocks up to {need_tok}")
+        kv.check_blocks(name, B * num_kv_heads, (max_len + BLOCK - 1) // BLOCK, tokens=max_len)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     ka = past_array(kv_len)
     need = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), ka, int(num_splits))

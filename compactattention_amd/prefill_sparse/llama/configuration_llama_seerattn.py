@@ -27,11 +27,15 @@ class SeerAttnLlamaConfig:
     rope_theta: float = 500000.0
     max_position_embeddings: int = 131072
     initializer_range: float = 0.02
-    # Seer AttnGate (attn_gate.py:37-112)
+    # Seer AttnGate (attn_gate.py:37-278).  The defaults are BASELINE config 1's gate (pooled
+    # Q and K, both projected per head); the reference's own default is Qavg_Kmaxminavg
+    # without force_double (configuration_llama_seerattn.py:191,198), and every
+    # Q{pools}_K{pools} type with either setting runs on the same kernels.
     seerattn_gate_type: str = "Qavg_Kavg"
     seerattn_gate_block_size: int = 64
     seerattn_gate_hidden_size: int = 128
     seerattn_gate_force_double: bool = True
+    seerattn_compactattn_kv_group_aware_gate: bool = False
     seerattn_sparsity_method: str = "threshold"
     seerattn_threshold: float = 5e-3
     seerattn_chunked_prefill_force_dense: bool = False
@@ -68,7 +72,10 @@ class SeerAttnLlamaConfig:
             raise ValueError("num_attention_heads must be a multiple of num_key_value_heads")
         if self.seerattn_gate_block_size != 64 or self.seerattn_flashprefill_block_size != 64:
             raise ValueError("the compactattn path runs 64-token blocks")
-        if self.seerattn_gate_type != "Qavg_Kavg" or not self.seerattn_gate_force_double:
-            raise ValueError("the AttnGate implemented here is Qavg_Kavg with force_double")
+        from ..attn_gate import parse_gate_type
+
+        parse_gate_type(self.seerattn_gate_type)
+        if self.seerattn_gate_hidden_size != 128:
+            raise ValueError("the gate kernels run a 128-dim gate hidden size")
         if self.seerattn_sparsity_method != "threshold":
             raise ValueError("the Seer selector implemented here is the softmax threshold")

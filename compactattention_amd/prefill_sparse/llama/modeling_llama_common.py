@@ -187,6 +187,26 @@ def dense_decode_forward(attn: nn.Module, hidden_states: torch.Tensor, position_
     return attn.o_proj(out.reshape(B, L, -1))
 
 
+def split_unaligned_chunk(attn: nn.Module, hidden_states: torch.Tensor, position_embeddings, past_key_value,
+                          attention_mask=None, **kwargs):
+    """A chunk of 64*n + r tokens (n >= 1, 0 < r < 64) over a block-aligned cache, e.g. the
+    last chunk of a prompt whose length is not a multiple of 64: its first 64*n tokens take
+    the module's chunk path (selection over whole blocks), then its last r tokens are one
+    dense step over the whole cache through the decode kernel (which reads the partial last
+    block up to the cache length only).  The reference instead pads the partial block and
+    keeps it selected for the whole chunk (compact_attn/modules/
+    attention_forward_chunked_dense.py:438-491); here the tail queries attend to every cached
+    key.  Returns the module's 5-tuple with the two parts' outputs concatenated."""
+    L = hidden_states.shape[1]
+    head_len = L - L % BLOCK
+    cos, sin = position_embeddings
+    head = attn.forward(hidden_states[:, :head_len], (cos[:head_len], sin[:head_len]), attention_mask,
+                        past_key_value=past_key_value, **kwargs)[0]
+    tail = dense_decode_forward(attn, hidden_states[:, head_len:], (cos[head_len:], sin[head_len:]),
+                                past_key_value.layer(attn.layer_idx))
+    return torch.cat([head, tail], dim=1), 0.0, None, None, None
+
+
 def is_decode_step(hidden_states: torch.Tensor, cache: PagedKVCache) -> bool:
     """Fewer than 64 new tokens, or a cache already past a block boundary, is decode."""
     return hidden_states.shape[1] < BLOCK or cache.length % BLOCK != 0
@@ -197,10 +217,15 @@ class ChunkedPrefillCache:
 
     def __init__(self, config: SeerAttnLlamaConfig, batch: int, max_tokens: int, device, with_kmean: bool,
                  with_kgate: bool):
+        from ..attn_gate import gate_key_heads
+
         max_tokens = -(-max_tokens // BLOCK) * BLOCK
+        kgate_heads = gate_key_heads(config.seerattn_gate_type, config.seerattn_gate_force_double,
+                                     config.seerattn_compactattn_kv_group_aware_gate, config.num_attention_heads,
+                                     config.num_key_value_heads)
         self.layers: List[PagedKVCache] = [
             PagedKVCache(batch, config.num_key_value_heads, max_tokens, device, with_kmean=with_kmean,
-                         with_kgate=with_kgate)
+                         with_kgate=with_kgate, kgate_heads=kgate_heads)
             for _ in range(config.num_hidden_layers)
         ]
 

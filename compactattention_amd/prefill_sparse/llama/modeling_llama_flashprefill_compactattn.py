@@ -26,7 +26,8 @@ from ...modules._core import COMPACTATTN_VERSION
 from ...modules.flashprefill_prefill import flashprefill_rule
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
-                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk)
+                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk,
+                                     split_unaligned_chunk)
 
 BLOCK = 64
 
@@ -72,7 +73,7 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
             return out, 0.0, None, None, None
         B, L, _ = hidden_states.shape
         if L % BLOCK:
-            raise ValueError("chunk lengths must be multiples of 64 tokens")
+            return split_unaligned_chunk(self, hidden_states, position_embeddings, past_key_value, attention_mask)
         q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
         with event_span(self.attention_timer):

@@ -10,9 +10,9 @@ attn_gate_output, ground_truth_mask); inference only.
 
 Execution per chunk (B requests advancing together, L tokens, P past blocks):
   1. paged append of RoPE'd K and V (ca_cache_fill, copy only);
-  2. gate K summaries of the new blocks from the pre-RoPE K (ca_cache_fill summaries:
-     block mean -> per-KV-head 128x128 projection -> block RoPE) into the cache's kgate;
-  3. pooled, projected, rotated query blocks (ca_pool_query with the gate's W_q);
+  2. gate K summaries of the new blocks from the pre-RoPE K (ca_gate_key_summaries: the
+     gate type's pools -> per-head projection -> block RoPE) into the cache's kgate;
+  3. pooled (projected, rotated) query blocks (ca_gate_query_summaries);
   4. gate scores + per-row rule (ca_score_select: softmax over causal key blocks,
      keep score > threshold, sink and local blocks);
   5. Q-block and GQA union into per-KV-group tables (ca_union_compact);
@@ -30,10 +30,11 @@ from torch import nn
 
 from ... import ops
 from ...modules._core import COMPACTATTN_VERSION
-from ..attn_gate import AttnGate
+from ..attn_gate import ATTNGATE_CLASSES
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
-                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk)
+                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk,
+                                     split_unaligned_chunk)
 
 BLOCK = 64
 
@@ -55,9 +56,11 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
         self.qkv = FusedProjections(self, ("q_proj", "k_proj", "v_proj"))
         self.attention_timer: Optional[list] = None  # a list collects timing events of the attention core
-        self.attn_gate = AttnGate(config.seerattn_gate_block_size, self.head_dim, config.seerattn_gate_hidden_size,
-                                  self.num_key_value_heads, self.num_heads,
-                                  force_double=config.seerattn_gate_force_double).to(device)
+        self.attn_gate = ATTNGATE_CLASSES[config.seerattn_gate_type](
+            config.seerattn_gate_block_size, self.head_dim, config.seerattn_gate_hidden_size,
+            num_k_head=self.num_key_value_heads, num_q_head=self.num_heads,
+            force_double=config.seerattn_gate_force_double,
+            kv_group_aware_query=config.seerattn_compactattn_kv_group_aware_gate).to(device)
         self.compactattn_keep_recent_blocks = config.seerattn_compactattn_keep_recent_blocks
         self.compactattn_version = COMPACTATTN_VERSION
         self.compactattn_debug = False
@@ -70,22 +73,20 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
 
     def _append_compactattn_chunked_gate_key_cache(self, key_states_nope: torch.Tensor, cache, past: int,
                                                    block_position_embeddings) -> None:
-        cos, sin = block_position_embeddings
-        B = key_states_nope.shape[0]
-        ops.cache_fill(key_states_nope, None, None, None, [past] * B, cache.cap, None,
-                       gate_wk=self.attn_gate.mask_linear_k.weight.detach(), rope_cos=cos, rope_sin=sin,
-                       kgate=cache.kgate)
+        self.attn_gate.compress_key_blocks(key_states_nope, out=cache.kgate, first_block=past,
+                                           position_embeddings=block_position_embeddings)
 
     def _select_tables(self, query_states_nope: torch.Tensor, cache, past: int, block_position_embeddings
                        ) -> Tuple[torch.Tensor, torch.Tensor]:
-        cos, sin = block_position_embeddings
+        """Gate scores per Q head (or per KV head for a kv-group-aware gate), threshold rule,
+        then the Q-block and GQA unions into per-KV-group tables."""
         B = query_states_nope.shape[0]
         P = [past] * B
-        qhat = ops.pool_query(query_states_nope, P, cache.cap,
-                              gate_wq=self.attn_gate.mask_linear_q.weight.detach(), rope_cos=cos, rope_sin=sin,
-                              num_kv_heads=self.num_key_value_heads)
-        rowmask, _ = ops.score_select(qhat, cache.kgate, self.attn_gate.scale, self._selection_rule(), P,
-                                      self.num_key_value_heads, cache.cap)
+        gate = self.attn_gate
+        qhat = gate.compress_query_blocks(query_states_nope, first_block=past,
+                                          position_embeddings=block_position_embeddings, kv_cap=cache.cap)
+        rowmask, _ = ops.score_select(qhat, cache.kgate, gate.scale, self._selection_rule(), P, gate.key_heads,
+                                      cache.cap)
         table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap)
         return table, counts
 
@@ -119,7 +120,8 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
             return out, 0.0, None, None, None
         B, L, _ = hidden_states.shape
         if L % BLOCK:
-            raise ValueError("chunk lengths must be multiples of 64 tokens")
+            return split_unaligned_chunk(self, hidden_states, position_embeddings, past_key_value, attention_mask,
+                                         block_position_embeddings=block_position_embeddings)
         q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
         with event_span(self.attention_timer):

@@ -19,6 +19,9 @@
  *     data + b*stride_b + kv_head*stride_h + phys(kb)*stride_blk + t*stride_tok + d
  * with phys(kb) = page_table ? page_table[(b*num_kv_heads + kv_head)*page_table_stride + kb]
  *                            : kb.
+ * stride_tok must be below 2^24 elements (a 64-token block spans < 2^31 bytes; CA_ERR_LIMIT
+ * otherwise).  A page table holds page ids in [0, num_pages); an id outside is clamped into
+ * the pool, so a corrupt table cannot address memory outside it.
  * This covers the reference's seq-first [B, K, Hkv, D] tensors, its heads-first
  * k_hf/v_hf [B, Hkv, K, D] cache (compact_attn/prefill_sparse/llama/
  * modeling_llama_seerattn_chunked_dense_hf.py:59-82, viewed as 64-token pages by
@@ -34,7 +37,7 @@
 extern "C" {
 #endif
 
-#define CA_ABI_VERSION 1
+#define CA_ABI_VERSION 2
 #define CA_HEAD_DIM 128
 #define CA_BLOCK 64
 #define CA_MAX_BATCH 64
@@ -77,6 +80,8 @@ typedef struct {
     int64_t stride_tok;
     const int32_t* page_table; /* optional (NULL: physical block = logical block) */
     int64_t page_table_stride;
+    int64_t num_pages; /* with a page table: pages in the pool; page ids read from the table
+                          are clamped into [0, num_pages) (ignored without a table)          */
 } ca_kv_layout;
 
 typedef struct {
@@ -133,6 +138,41 @@ int ca_cache_fill(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_
 int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* past_blocks_host,
                   const float* gate_wq, const float* rope_cos, const float* rope_sin,
                   int64_t rope_rows, float* qhat, void* stream);
+
+/*
+ * AttnGate block summaries for every gate type of the reference (compact_attn/prefill_sparse/
+ * attn_gate.py:37-130,233-278: the Q{pools}_K{pools} classes, force_double, the
+ * kv_group_aware_query form).  pools is a set of CA_POOL_* bits; the pooled vectors of a
+ * 64-token block (max and min of the bf16 values, avg = sequential sum times 1/64) are
+ * concatenated in the order max, min, avg into an input of in = C*128 values (C pools), then
+ * projected, y[o] = sum_{i < in} x[i] W[i][o] (sequential fma over i), and rotated at the
+ * block's absolute id (rope_cos/rope_sin [rope_rows, 128], may be NULL).
+ *
+ * ca_gate_key_summaries: the new blocks of k_new ([B, q_len, Hkv, 128]) -> kgate rows
+ * (b*gate_heads + j)*kv_cap + past_blocks[b] + n.  gate_heads = num_kv_heads: W_k
+ * [Hkv, in, 128] per KV head; gate_heads = num_q_heads: the block is repeated to the G Q
+ * heads of its group (head hk*G + j) and projected per Q head with W_k [Hq, in, 128] -- the
+ * reference's single-linear gate (attn_gate.py:84-86 with MultiHeadLinear's repeat, :30-33).
+ * ca_gate_query_summaries: the query blocks of q ([B, q_len, Hq, 128]) -> qhat
+ * [B, gate_heads, q_len/64, 128].  gate_wq NULL: no projection (one pool only, gate_heads =
+ * num_q_heads; the pooled vector is still rotated when rope tables are given, as the
+ * reference rotates its unprojected query blocks).  gate_heads = num_q_heads: W_q
+ * [Hq, in, 128] per Q head.  gate_heads =
+ * num_kv_heads (kv_group_aware_query): the G heads of a KV group are pooled and concatenated
+ * head-major into G*in values and projected with W_q [Hkv, G*in, 128].
+ * Replaces: AttnGate.compress_query_blocks / compress_key_blocks / MultiHeadLinear /
+ * apply_block_position_embeddings (attn_gate.py:20-34,113-171) and the gate K-block cache
+ * append (compact_attn/prefill_sparse/llama/modeling_llama_seerattn.py:407-435).
+ */
+#define CA_POOL_MAX 1
+#define CA_POOL_MIN 2
+#define CA_POOL_AVG 4
+int ca_gate_key_summaries(const ca_dims* dims, const ca_seq_layout* k_new, const int32_t* past_blocks_host,
+                          int32_t pools, const float* gate_wk, int32_t gate_heads, const float* rope_cos,
+                          const float* rope_sin, int64_t rope_rows, float* kgate, void* stream);
+int ca_gate_query_summaries(const ca_dims* dims, const ca_seq_layout* q, const int32_t* past_blocks_host,
+                            int32_t pools, const float* gate_wq, int32_t gate_heads, const float* rope_cos,
+                            const float* rope_sin, int64_t rope_rows, float* qhat, void* stream);
 
 /*
  * Block scoring and per-row selection.  For every (b, h, qb) row it computes

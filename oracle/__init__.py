@@ -134,21 +134,47 @@ def block_mean(x_bits: np.ndarray) -> np.ndarray:
     return out
 
 
+POOL_MAX = 1
+POOL_MIN = 2
+POOL_AVG = 4
+POOL_BITS = {"max": POOL_MAX, "min": POOL_MIN, "avg": POOL_AVG}
+
+
+def pool_bits(names) -> int:
+    """('max', 'avg') -> POOL_MAX | POOL_AVG (the concatenation order is always max, min, avg)."""
+    bits_ = 0
+    for nm in names:
+        bits_ |= POOL_BITS[nm]
+    return bits_
+
+
+def block_pool(x_bits: np.ndarray, pools: int) -> np.ndarray:
+    """x: [B, L, H, 128] bf16 bits -> [B, H, L/64, C*128] fp32 (max, min, avg as selected)."""
+    x = np.ascontiguousarray(x_bits, dtype=np.uint16)
+    B, L, H, d = x.shape
+    assert d == D and L % BLOCK == 0 and 0 < pools < 8
+    C = bin(pools).count("1")
+    out = np.empty((B, H, L // BLOCK, C * D), dtype=np.float32)
+    lib().orc_block_pool(_p(x), B, L, H, int(pools), _p(out))
+    return out
+
+
 def gate_project(x: np.ndarray, W: np.ndarray, cos: Optional[np.ndarray], sin: Optional[np.ndarray],
                  first_block) -> np.ndarray:
-    """x: [B, H, N, 128] fp32; W: [H, 128, 128]; cos/sin: [rows, 128] by absolute block id."""
+    """x: [B, H, N, in] fp32; W: [H, in, 128]; cos/sin: [rows, 128] by absolute block id."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     W = np.ascontiguousarray(W, dtype=np.float32)
-    B, H, N, _ = x.shape
+    B, H, N, width = x.shape
+    assert W.shape == (H, width, D)
     fb = _i32(first_block)
-    y = np.empty_like(x)
+    y = np.empty((B, H, N, D), dtype=np.float32)
     if cos is None:
-        lib().orc_gate_project(_p(x), B, H, N, _p(W), None, None, ctypes.c_int64(0), _p(fb), _p(y))
+        lib().orc_gate_project_n(_p(x), B, H, N, width, _p(W), None, None, ctypes.c_int64(0), _p(fb), _p(y))
     else:
         c = np.ascontiguousarray(cos, dtype=np.float32)
         s = np.ascontiguousarray(sin, dtype=np.float32)
-        lib().orc_gate_project(_p(x), B, H, N, _p(W), _p(c), _p(s), ctypes.c_int64(c.shape[0]),
-                               _p(fb), _p(y))
+        lib().orc_gate_project_n(_p(x), B, H, N, width, _p(W), _p(c), _p(s), ctypes.c_int64(c.shape[0]),
+                                 _p(fb), _p(y))
     return y
 
 

@@ -106,18 +106,50 @@ void orc_block_mean(const uint16_t* x, int B, int L, int H, float* out) {
                 }
 }
 
+void orc_block_pool(const uint16_t* x, int B, int L, int H, int pools, float* out) {
+    const int nb = L / ORC_BLOCK;
+    int C = 0;
+    for (int bit = 1; bit <= ORC_POOL_AVG; bit <<= 1) C += (pools & bit) ? 1 : 0;
+    for (int b = 0; b < B; ++b)
+        for (int h = 0; h < H; ++h)
+            for (int n = 0; n < nb; ++n) {
+                float* o = out + (((int64_t)b * H + h) * nb + n) * (int64_t)C * ORC_D;
+                for (int d = 0; d < ORC_D; ++d) {
+                    const uint16_t* xs = x + ((((int64_t)b * L + (int64_t)n * ORC_BLOCK) * H) + h) * ORC_D + d;
+                    const int64_t st = (int64_t)H * ORC_D;
+                    float mx = orc_bf16_to_f32(xs[0]), mn = mx, s = 0.0f;
+                    for (int t = 0; t < ORC_BLOCK; ++t) {
+                        const float v = orc_bf16_to_f32(xs[t * st]);
+                        mx = v > mx ? v : mx;
+                        mn = v < mn ? v : mn;
+                        s = s + v;
+                    }
+                    int c = 0;
+                    if (pools & ORC_POOL_MAX) o[(c++) * ORC_D + d] = mx;
+                    if (pools & ORC_POOL_MIN) o[(c++) * ORC_D + d] = mn;
+                    if (pools & ORC_POOL_AVG) o[(c++) * ORC_D + d] = s * 0.015625f;
+                }
+            }
+}
+
 void orc_gate_project(const float* x, int B, int H, int N, const float* W,
                       const float* cos_t, const float* sin_t, int64_t rope_rows,
                       const int32_t* first_block, float* y) {
+    orc_gate_project_n(x, B, H, N, ORC_D, W, cos_t, sin_t, rope_rows, first_block, y);
+}
+
+void orc_gate_project_n(const float* x, int B, int H, int N, int in, const float* W,
+                        const float* cos_t, const float* sin_t, int64_t rope_rows,
+                        const int32_t* first_block, float* y) {
     float proj[ORC_D];
     for (int b = 0; b < B; ++b)
         for (int h = 0; h < H; ++h)
             for (int n = 0; n < N; ++n) {
-                const float* xv = x + (((int64_t)b * H + h) * N + n) * ORC_D;
-                const float* w = W + (int64_t)h * ORC_D * ORC_D;
+                const float* xv = x + (((int64_t)b * H + h) * N + n) * (int64_t)in;
+                const float* w = W + (int64_t)h * in * ORC_D;
                 for (int o = 0; o < ORC_D; ++o) {
                     float acc = 0.0f;
-                    for (int i = 0; i < ORC_D; ++i) acc = fmaf(xv[i], w[(int64_t)i * ORC_D + o], acc);
+                    for (int i = 0; i < in; ++i) acc = fmaf(xv[i], w[(int64_t)i * ORC_D + o], acc);
                     proj[o] = acc;
                 }
                 float* yv = y + (((int64_t)b * H + h) * N + n) * ORC_D;

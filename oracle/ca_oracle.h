@@ -50,6 +50,18 @@ uint16_t orc_f32_to_bf16(float v);
 /* x: [B, L, H, 128] bf16 (L % 64 == 0) -> out: [B, H, L/64, 128] fp32 block means. */
 void orc_block_mean(const uint16_t* x, int B, int L, int H, float* out);
 
+/* Gate pooling set (AttnGate pooling functions, compact_attn/prefill_sparse/attn_gate.py:
+ * 233-237): the pooled vectors are concatenated in the order max, min, avg. */
+#define ORC_POOL_MAX 1
+#define ORC_POOL_MIN 2
+#define ORC_POOL_AVG 4
+
+/* Block pooling over 64 tokens: x [B, L, H, 128] bf16 -> out [B, H, L/64, C*128] fp32 with
+ * C = popcount(pools); max and min keep the bf16 values, avg is the sequential sum times 1/64
+ * (as orc_block_mean).  max/min are strict compares from token 0 (the first of equal values
+ * stays). */
+void orc_block_pool(const uint16_t* x, int B, int L, int H, int pools, float* out);
+
 /* Per-head gate projection followed by block RoPE.
  * x: [B, H, N, 128] fp32, W: [H, 128, 128] (in, out), cos/sin: [rope_rows, 128]
  * indexed by absolute block id; block n of request b has id first_block[b] + n.
@@ -57,6 +69,12 @@ void orc_block_mean(const uint16_t* x, int B, int L, int H, float* out);
 void orc_gate_project(const float* x, int B, int H, int N, const float* W,
                       const float* cos_t, const float* sin_t, int64_t rope_rows,
                       const int32_t* first_block, float* y);
+
+/* The same with an input width `in` (x [B, H, N, in], W [H, in, 128]); the sum over the
+ * input runs i = 0 .. in-1 in order. */
+void orc_gate_project_n(const float* x, int B, int H, int N, int in, const float* W,
+                        const float* cos_t, const float* sin_t, int64_t rope_rows,
+                        const int32_t* first_block, float* y);
 
 /* Softmax-normalised block scores.
  * qhat: [B, Hq, Qb, 128], khat: [B, Hkv, cap, 128]; scores: [B, Hq, Qb, cap].

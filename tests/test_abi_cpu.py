@@ -34,7 +34,7 @@ def test_header_matches_exports():
 
 def test_library_loads_and_reports_version():
     lib = _hip.lib()
-    assert lib.ca_abi_version() == _hip.ABI_VERSION == 1
+    assert lib.ca_abi_version() == _hip.ABI_VERSION == 2
 
 
 def _dims(**kw):
@@ -51,7 +51,7 @@ def _seq(data=FAKE, sb=0, st=1024, sh=128):
 
 
 def _kv(data=FAKE, sb=0, sh=0, sblk=8192, stok=128):
-    return _hip.KvLayout(data, sb, sh, sblk, stok, None, 0)
+    return _hip.KvLayout(data, sb, sh, sblk, stok, None, 0, 0)
 
 
 def _past(*p):
@@ -178,10 +178,51 @@ def test_cache_fill_validation():
     rc = lib.ca_cache_fill(ctypes.byref(d), ctypes.byref(_seq()), ctypes.byref(_seq()), ctypes.byref(_kv()),
                            ctypes.byref(_kv()), _past(0), FAKE, FAKE, None, None, 0, None, None)
     assert rc == _hip.CA_ERR_INVALID and "kgate" in _hip.last_error()
-    pt = _hip.KvLayout(FAKE, 0, 0, 8192, 128, FAKE, 1)
+    pt = _hip.KvLayout(FAKE, 0, 0, 8192, 128, FAKE, 1, 8)
     rc = lib.ca_cache_fill(ctypes.byref(d), ctypes.byref(_seq()), ctypes.byref(_seq()), ctypes.byref(pt),
                            ctypes.byref(_kv()), _past(0), FAKE, None, None, None, 0, None, None)
     assert rc == _hip.CA_ERR_INVALID and "page_table_stride" in _hip.last_error()
+    # a page table needs the pool's page count (ids are clamped into it)
+    nopages = _hip.KvLayout(FAKE, 0, 0, 8192, 128, FAKE, 10, 0)
+    rc = lib.ca_cache_fill(ctypes.byref(d), ctypes.byref(_seq()), ctypes.byref(_seq()), ctypes.byref(nopages),
+                           ctypes.byref(_kv()), _past(0), FAKE, None, None, None, 0, None, None)
+    assert rc == _hip.CA_ERR_INVALID and "num_pages" in _hip.last_error()
+
+
+def test_token_stride_limit():
+    """The kernels address a block's 64 rows with 32-bit byte offsets: stride_tok >= 2^24 is
+    refused (CA_ERR_LIMIT) by every entry point that reads or writes a KV layout."""
+    lib = _hip.lib()
+    d = _dims()
+    big = _kv(stok=1 << 24, sblk=64 << 24)
+    rc = lib.ca_cache_fill(ctypes.byref(d), ctypes.byref(_seq()), ctypes.byref(_seq()), ctypes.byref(big),
+                           ctypes.byref(_kv()), _past(0), FAKE, None, None, None, 0, None, None)
+    assert rc == _hip.CA_ERR_LIMIT and "stride_tok" in _hip.last_error()
+    ok = _kv(stok=(1 << 24) - 8, sblk=64 * ((1 << 24) - 8))
+    rc = lib.ca_attn_fwd(ctypes.byref(d), ctypes.byref(_seq()), ctypes.byref(big), ctypes.byref(ok), FAKE, 10, FAKE,
+                         _past(0), 0.1, ctypes.byref(_seq()), None, 1, None, 0, None)
+    assert rc == _hip.CA_ERR_LIMIT and "stride_tok" in _hip.last_error()
+    kvl = (ctypes.c_int32 * 1)(100)
+    rc = lib.ca_attn_decode(ctypes.byref(_dims(q_len=1)), ctypes.byref(_seq()), ctypes.byref(ok), ctypes.byref(big),
+                            kvl, 0.1, ctypes.byref(_seq()), None, 1, None, 0, None)
+    assert rc == _hip.CA_ERR_LIMIT and "stride_tok" in _hip.last_error()
+
+
+def test_gate_summary_validation():
+    lib = _hip.lib()
+    d = _dims()  # Hq 8, Hkv 2
+    call_k = lambda pools, heads, w=FAKE, out=FAKE: lib.ca_gate_key_summaries(  # noqa: E731
+        ctypes.byref(d), ctypes.byref(_seq()), _past(0), pools, w, heads, None, None, 0, out, None)
+    assert call_k(0, 2) == _hip.CA_ERR_INVALID and "pools" in _hip.last_error()
+    assert call_k(8, 2) == _hip.CA_ERR_INVALID and "pools" in _hip.last_error()
+    assert call_k(7, 3) == _hip.CA_ERR_INVALID and "gate_heads" in _hip.last_error()
+    assert call_k(7, 2, w=None) == _hip.CA_ERR_INVALID
+    call_q = lambda pools, heads, w=FAKE: lib.ca_gate_query_summaries(  # noqa: E731
+        ctypes.byref(d), ctypes.byref(_seq()), _past(0), pools, w, heads, None, None, 0, FAKE, None)
+    # several pools need a projection; an unprojected summary has one head per Q head
+    assert call_q(_hip.POOL_MAX | _hip.POOL_AVG, 8, w=None) == _hip.CA_ERR_INVALID and "projection" in _hip.last_error()
+    assert call_q(_hip.POOL_AVG, 2, w=None) == _hip.CA_ERR_INVALID and "gate_heads" in _hip.last_error()
+    assert call_q(_hip.POOL_AVG, 4) == _hip.CA_ERR_INVALID and "gate_heads" in _hip.last_error()
 
 
 def test_python_entry_points_reject_bad_arguments():
@@ -203,8 +244,11 @@ def test_python_entry_points_reject_bad_arguments():
         f(q, k, k, None, 128, attn_gate_score=gate, indexed_impl="nope")
     with pytest.raises(ValueError, match="64-token blocks"):
         f(q, k, k, None, 128, attn_gate_score=gate, block_size=128, num_key_value_groups=4)
-    with pytest.raises(ValueError, match="multiples of 64"):
+    # an unaligned call splits into an aligned head and a dense tail; its chunk must start on a block
+    with pytest.raises(ValueError, match="block boundary"):
         f(q, k[:, :600], k[:, :600], None, 128, attn_gate_score=gate, num_key_value_groups=4)
+    with pytest.raises(ValueError, match="does not match query_states"):
+        f(q[:, :100], k, k, None, 128, attn_gate_score=gate, num_key_value_groups=4)
     with pytest.raises(ValueError, match="per-request threshold"):
         f(q, k, k, None, 128, attn_gate_score=gate, threshold=torch.zeros(2), num_key_value_groups=4)
     with pytest.raises(ValueError, match="Either keep_block"):

@@ -21,10 +21,10 @@ from compactattention_amd.modules.attention_forward_chunked_dense import (
     chunked_prefill_column_dense_attention_forward, chunked_prefill_column_dense_attention_from_keep_block)
 from compactattention_amd.modules.flashprefill_prefill import (flashprefill_compactattn_prefill_full_kv,
                                                                flashprefill_rule)
-from compactattention_amd.prefill_sparse.attn_gate import AttnGate
+from compactattention_amd.prefill_sparse.attn_gate import ATTNGATE_CLASSES
 from compactattention_amd.synthetic import make_chunk, rope_tables
 
-from .util import bits, f32, float_bits_equal, ref_flashprefill_tables
+from .util import bits, f32, float_bits_equal, oracle_gate_summaries, ref_flashprefill_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -139,6 +139,76 @@ def test_flashprefill_entry(gpu, params):
     _check_attention(out, ch, ref_table, ref_counts)
 
 
+@pytest.mark.parametrize("q_len", [1, 37, 256 + 37])
+def test_unaligned_entries(gpu, q_len):
+    """Calls whose q_len is not a multiple of 64 (the chunk starting on a block): fewer than 64
+    queries attend densely to all kv_len keys (the reference's dense fallback); a longer chunk
+    selects for its aligned head (the reference's tables over the head's keys) and its last
+    q_len % 64 queries attend densely -- for the FlashPrefill entry and both Seer entries."""
+    _print_case(test="unaligned_entries", q_len=q_len)
+    Hq, Hkv, past = 8, 2, 64 * 20
+    G = Hq // Hkv
+    kv_len = past + q_len
+    head = 0 if q_len < 64 else q_len - q_len % 64
+    g = torch.Generator().manual_seed(q_len)
+    q = torch.randn((1, q_len, Hq, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, kv_len, Hkv, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, kv_len, Hkv, 128), generator=g).to(torch.bfloat16)
+    khf, vhf = k.transpose(1, 2).contiguous(), v.transpose(1, 2).contiguous()
+
+    def check(out, table=None, counts=None):
+        got = f32(out)
+        if head:
+            ref = oracle.attention(bits(q[:, :head]), bits(khf[:, :, :past + head]), bits(vhf[:, :, :past + head]),
+                                   [past // 64], table, counts, SCALE)
+            err = np.abs(got[:, :head] - ref)
+            assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, ("head", err.max(), err.mean())
+        ref = oracle.attention_decode(bits(q[:, head:].contiguous()), bits(khf), bits(vhf), [kv_len], SCALE)
+        err = np.abs(got[:, head:] - ref)
+        assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, ("tail", err.max(), err.mean())
+
+    # FlashPrefill: the head's tables are the reference's rowwise selection over its keys
+    fp = dict(attention_sink=1, window_size=2, alpha=0.3, last_n_block=0, min_budget=4)
+    out, stats = flashprefill_compactattn_prefill_full_kv(
+        q.to(gpu), k.to(gpu), v.to(gpu), None, softmax_scale=SCALE, num_key_value_groups=G, block_size=64,
+        pack_impl="indexed_dense", indexed_impl="fi_zero_copy", cache_fill_backend="auto", **fp)
+    assert stats["flashprefill_dense_tail_tokens"] == q_len - head
+    table = counts = None
+    if head:
+        sc = oracle.block_scores(oracle.block_mean(bits(q[:, :head])), oracle.block_mean(bits(k[:, :past + head])),
+                                 [past // 64], SCALE)
+        table, counts = ref_flashprefill_tables(sc, [past // 64], Hkv, fp["alpha"], fp["attention_sink"],
+                                                fp["window_size"], fp["min_budget"], fp["last_n_block"])
+    check(out, table, counts)
+    if q_len < 2:
+        return  # the Seer entries require query_length > 1 (as the reference's)
+    # Seer: threshold on caller gate scores over the head's blocks
+    nqb, nkb = -(-q_len // 64), -(-kv_len // 64)
+    gate = torch.rand((1, Hq, nqb, nkb), generator=g) * 0.1
+    out, _ = chunked_prefill_column_dense_attention_forward(
+        q.to(gpu), k.to(gpu), v.to(gpu), None, q_len, softmax_scale=SCALE, attn_gate_score=gate.to(gpu),
+        threshold=0.08, num_key_value_groups=G, pack_impl="indexed_dense", indexed_impl="fi_zero_copy")
+    if head:
+        hg = gate[:, :, :head // 64, :(past + head) // 64].contiguous().numpy()
+        keep = oracle.select_rows(hg, [past // 64], oracle.Rule(threshold=0.08))
+        _, _, table, counts = oracle.union_compact(keep, Hkv, [past // 64])
+    check(out, table, counts)
+    keep_block = torch.rand((1, Hq, nkb), generator=g) < 0.3
+    out, _ = chunked_prefill_column_dense_attention_from_keep_block(
+        q.to(gpu), k.to(gpu), v.to(gpu), keep_block.to(gpu), None, q_len, SCALE, num_key_value_groups=G)
+    if head:
+        cap = (past + head) // 64
+        kv = keep_block[:, :, :cap].view(1, Hkv, G, cap).any(dim=2).numpy().astype(np.uint8)
+        kv[..., past // 64:] = 1
+        table = np.full((Hkv, cap), -1, np.int32)
+        counts = np.zeros((Hkv,), np.int32)
+        for h in range(Hkv):
+            ids = np.nonzero(kv[0, h])[0]
+            table[h, :len(ids)] = ids
+            counts[h] = len(ids)
+    check(out, table, counts)
+
+
 def test_flashprefill_first_chunk_is_dense(gpu):
     _print_case(test="flashprefill_first_chunk")
     ch = make_chunk([0], 128, 4, 2, seed=6)
@@ -163,19 +233,34 @@ def test_flashprefill_scores_bit_exact(gpu):
     assert float_bits_equal(f32(sc.permute(0, 3, 1, 2)), ref)
 
 
-def test_attn_gate_bit_exact(gpu):
-    _print_case(test="attn_gate")
+GATE_CASES = [
+    # (gate type, force_double, kv_group_aware_query)
+    ("Qavg_Kavg", True, False),          # BASELINE config 1's gate
+    ("Qavg_Kmaxminavg", False, False),   # the reference's default: no query projection, W_k per Q head
+    ("Qavg_Kmaxminavg", True, False),
+    ("Qmaxavg_Kmax", False, False),      # two query pools: projected per Q head
+    ("Qavg_Kmaxminavg", False, True),    # kv-group-aware query, scores per KV head
+]
+
+
+@pytest.mark.parametrize("case", GATE_CASES, ids=lambda c: f"{c[0]}-fd{int(c[1])}-kv{int(c[2])}")
+def test_attn_gate_bit_exact(gpu, case):
+    """AttnGate scores for the reference's gate types against the oracle composition: pooling
+    (max/min/avg, concatenated in that order), the reference's projection case for the type
+    (attn_gate.py:74-86), block RoPE, q.k^T * 128^-1/2, causal softmax -- bit for bit."""
+    gate_type, force_double, kv_aware = case
+    _print_case(test="attn_gate", gate_type=gate_type, force_double=force_double, kv_aware=kv_aware)
     Hq, Hkv, Lq, past = 8, 2, 128, 64 * 12
     ch = make_chunk([past], Lq, Hq, Hkv, seed=8)
-    gate = AttnGate(64, 128, 128, Hkv, Hq).to(gpu)
+    gate = ATTNGATE_CLASSES[gate_type](64, 128, 128, Hkv, Hq, force_double=force_double,
+                                       kv_group_aware_query=kv_aware).to(gpu)
     gate.reset_parameters(0.02, torch.Generator().manual_seed(2))
     cos, sin = rope_tables(ch.kv_cap)
     scores = gate(ch.q.to(gpu), _seq_first(ch.k).to(gpu), position_embeddings=(cos.to(gpu), sin.to(gpu)))
-    wq = f32(gate.mask_linear_q.weight)
-    wk = f32(gate.mask_linear_k.weight)
     P = ch.past_blocks
-    qg = oracle.gate_project(oracle.block_mean(bits(ch.q)), wq, f32(cos), f32(sin), P)
-    kg = oracle.gate_project(oracle.block_mean(bits(_seq_first(ch.k))), wk, f32(cos), f32(sin), [0])
+    assert gate.key_heads == (Hq if (gate_type == "Qavg_Kmaxminavg" and not force_double and not kv_aware) else Hkv)
+    qg, kg = oracle_gate_summaries(gate, bits(ch.q), bits(_seq_first(ch.k)), f32(cos), f32(sin), P[0])
+    assert tuple(scores.shape) == (1, gate.query_heads, Lq // 64, ch.kv_cap)
     ref = oracle.block_scores(qg, kg, P, 128 ** -0.5)
     assert float_bits_equal(f32(scores), ref)
 

@@ -108,6 +108,79 @@ def test_pool_query_bit_exact(gpu, gate):
     assert float_bits_equal(f32(qhat), ref)
 
 
+# ----------------------------------------------------------------------------- AttnGate summaries
+GATE_POOLS = [("avg",), ("max",), ("min", "avg"), ("max", "min", "avg")]
+
+
+@pytest.mark.parametrize("per_q_head", [False, True])
+@pytest.mark.parametrize("pools", GATE_POOLS, ids=lambda p: "".join(p))
+def test_gate_key_summaries_bit_exact(gpu, pools, per_q_head):
+    """K pools -> projection (per KV head, or per Q head on the K block repeated to the
+    group's Q heads) -> block RoPE, bit for bit against the oracle."""
+    _print_case(test="gate_key_summaries", pools=pools, per_q_head=per_q_head)
+    B, Lq, Hkv, G, past = 2, 192, 2, 3, [4, 7]
+    Hq = Hkv * G
+    qb = Lq // 64
+    cap = max(past) + qb + 1
+    C = len(pools)
+    gh = Hq if per_q_head else Hkv
+    g = torch.Generator().manual_seed(31 + C)
+    k_new = torch.randn((B, Lq, Hkv, 128), generator=g).to(torch.bfloat16)
+    wk = (torch.randn((gh, C * 128, 128), generator=g) * 0.02).float()
+    cos, sin = rope_tables(cap)
+    kgate = torch.full((B, gh, cap, 128), float("nan"), device=gpu)
+    ops.gate_key_summaries(k_new.to(gpu), past, cap, ops.pool_bits(pools), wk.to(gpu), kgate, num_q_heads=Hq,
+                           rope_cos=cos.to(gpu), rope_sin=sin.to(gpu))
+    pooled = oracle.block_pool(bits(k_new), oracle.pool_bits(pools))  # [B, Hkv, qb, C*128]
+    if per_q_head:
+        pooled = np.repeat(pooled, G, axis=1)
+    ref = oracle.gate_project(pooled, f32(wk), f32(cos), f32(sin), past)
+    got = f32(kgate)
+    for b in range(B):
+        assert float_bits_equal(got[b, :, past[b]:past[b] + qb], ref[b])
+        assert np.isnan(got[b, :, :past[b]]).all()  # nothing outside the new blocks is written
+
+
+@pytest.mark.parametrize("mode", ["none", "per_q_head", "kv_group_aware"])
+@pytest.mark.parametrize("pools", GATE_POOLS, ids=lambda p: "".join(p))
+def test_gate_query_summaries_bit_exact(gpu, pools, mode):
+    """Q pools -> no projection / per-Q-head projection / kv-group-aware projection of the
+    group's concatenated pooled heads -> block RoPE, bit for bit against the oracle."""
+    if mode == "none" and len(pools) > 1:
+        pytest.skip("several query pools always have a projection (attn_gate.py:80-86)")
+    _print_case(test="gate_query_summaries", pools=pools, mode=mode)
+    B, Lq, Hkv, G, past = 2, 128, 2, 4, [3, 10]
+    Hq = Hkv * G
+    qb = Lq // 64
+    cap = max(past) + qb
+    C = len(pools)
+    g = torch.Generator().manual_seed(57 + C)
+    q = torch.randn((B, Lq, Hq, 128), generator=g).to(torch.bfloat16)
+    cos, sin = rope_tables(cap)
+    pooled = oracle.block_pool(bits(q), oracle.pool_bits(pools))  # [B, Hq, qb, C*128]
+    if mode == "none":
+        got = ops.gate_query_summaries(q.to(gpu), past, cap, ops.pool_bits(pools), None, Hkv)
+        assert float_bits_equal(f32(got), pooled)
+        # no projection but the block RoPE (the reference's default gate): the identity
+        # projection in the oracle reproduces the pooled vector exactly before the rotation
+        got = ops.gate_query_summaries(q.to(gpu), past, cap, ops.pool_bits(pools), None, Hkv,
+                                       rope_cos=cos.to(gpu), rope_sin=sin.to(gpu))
+        eye = np.tile(np.eye(128, dtype=np.float32), (Hq, 1, 1))
+        ref = oracle.gate_project(pooled, eye, f32(cos), f32(sin), past)
+    elif mode == "per_q_head":
+        wq = (torch.randn((Hq, C * 128, 128), generator=g) * 0.02).float()
+        got = ops.gate_query_summaries(q.to(gpu), past, cap, ops.pool_bits(pools), wq.to(gpu), Hkv,
+                                       rope_cos=cos.to(gpu), rope_sin=sin.to(gpu))
+        ref = oracle.gate_project(pooled, f32(wq), f32(cos), f32(sin), past)
+    else:
+        wq = (torch.randn((Hkv, G * C * 128, 128), generator=g) * 0.02).float()
+        got = ops.gate_query_summaries(q.to(gpu), past, cap, ops.pool_bits(pools), wq.to(gpu), Hkv,
+                                       rope_cos=cos.to(gpu), rope_sin=sin.to(gpu))
+        cat = pooled.reshape(B, Hkv, G, qb, C * 128).transpose(0, 1, 3, 2, 4).reshape(B, Hkv, qb, G * C * 128)
+        ref = oracle.gate_project(cat, f32(wq), f32(cos), f32(sin), past)
+    assert float_bits_equal(f32(got), ref)
+
+
 # ----------------------------------------------------------------------------- scoring + selection
 RULES = {
     "topk_sink_local": oracle.Rule(topk=5, sink_blocks=1, local_blocks=2),
@@ -450,8 +523,19 @@ def test_decode_equals_prefill_on_aligned_shapes(gpu):
     assert torch.equal(pre_lse, dec_lse)
 
 
-def test_decode_rejects_short_contiguous_cache(gpu):
-    q = torch.zeros((1, 1, 2, 128), dtype=torch.bfloat16, device=gpu)
-    k = torch.zeros((1, 1, 100, 128), dtype=torch.bfloat16, device=gpu)
-    with pytest.raises(ValueError, match="whole blocks"):
-        ops.attn_decode(q, ops.KV.heads_first(k), ops.KV.heads_first(k), [100], 0.1, 2, 1)
+def test_decode_cache_ending_at_kv_len(gpu):
+    """The decode kernel's reads stop at kv_len (the partial last block's buffer range ends
+    there), so a contiguous cache holding exactly kv_len tokens is valid; one token short is
+    refused on the host."""
+    _print_case(test="decode_exact_cache")
+    g = torch.Generator().manual_seed(23)
+    q = torch.randn((1, 3, 4, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((1, 2, 100, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((1, 2, 100, 128), generator=g).to(torch.bfloat16)
+    K, V = ops.KV.heads_first(k.to(gpu)), ops.KV.heads_first(v.to(gpu))
+    out = ops.attn_decode(q.to(gpu), K, V, [100], 0.1, 2, 2)
+    ref = oracle.attention_decode(bits(q), bits(k), bits(v), [100], 0.1)
+    err = np.abs(f32(out) - ref)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
+    with pytest.raises(ValueError, match="holds 100 tokens"):
+        ops.attn_decode(q.to(gpu), K, V, [101], 0.1, 2, 2)

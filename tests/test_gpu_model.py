@@ -23,7 +23,7 @@ from compactattention_amd.prefill_sparse.llama import (SeerAttnLlamaChunkedDense
                                                        SeerAttnLlamaFlashPrefillCompactAttnForCausalLM)
 from compactattention_amd.prefill_sparse.llama.modeling_llama_common import apply_rotary_pos_emb, project_qkv
 
-from .util import bits, f32
+from .util import bits, f32, oracle_gate_summaries
 
 pytestmark = pytest.mark.gpu
 
@@ -47,8 +47,9 @@ def _model(cls, gpu, qk_scale: float = 1.0, gate_scale: float = 1.0, **kw):
             layer.self_attn.q_proj.weight.mul_(qk_scale)
             layer.self_attn.k_proj.weight.mul_(qk_scale)
             if hasattr(layer.self_attn, "attn_gate"):
-                layer.self_attn.attn_gate.mask_linear_q.weight.mul_(gate_scale)
-                layer.self_attn.attn_gate.mask_linear_k.weight.mul_(gate_scale)
+                for lin in (layer.self_attn.attn_gate.mask_linear_q, layer.self_attn.attn_gate.mask_linear_k):
+                    if lin is not None:
+                        lin.weight.mul_(gate_scale)
     return m
 
 
@@ -132,6 +133,31 @@ def test_decode_steps_match_fp32_reference(gpu, cls):
         m(ids[:, :128], cache)
 
 
+@pytest.mark.parametrize("cls", [SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaFlashPrefillCompactAttnForCausalLM])
+def test_unaligned_prompt_matches_fp32_reference(gpu, cls):
+    """A prompt of 64*n + 37 tokens: the last chunk's aligned part takes the chunk path and its
+    37-token tail one dense decode step; the last logits match the fp32 CPU forward, a decode
+    step continues from the unaligned length, and a keep-all Seer selection equals the dense
+    run bit for bit."""
+    print(f"case: model unaligned prompt {cls.__name__}", flush=True)
+    n = T + 37
+    m = _model(cls, gpu, seerattn_chunked_prefill_force_dense=True)
+    ids = synthetic_prompt(1, n + 1, m.config.vocab_size, 2024, gpu)
+    cache = m.new_cache(1, n + 64)
+    logits, _ = run_chunked_prefill_once(m, ids[:, :n], CHUNK, cache)
+    assert cache.get_seq_length() == n
+    for upto, got in ((n, logits), (n + 1, m(ids[:, n:n + 1], cache))):
+        ref = _reference_logits(m, ids[:, :upto])
+        got = got.float().cpu()
+        cos = F.cosine_similarity(got.flatten(), ref.flatten(), dim=0).item()
+        assert cos > 0.999, (upto, cos)
+        assert (got - ref).abs().max().item() <= 0.05 * ref.abs().max().item()
+    if cls is SeerAttnLlamaChunkedDenseForCausalLM:
+        keep_all = _model(cls, gpu, seerattn_threshold=-1.0)
+        b, _ = run_chunked_prefill_once(keep_all, ids[:, :n], CHUNK)
+        assert torch.equal(logits, b)
+
+
 @pytest.mark.parametrize("variant", ["seer_compactattn", "flashprefill_compactattn"])
 def test_hf_replacement_matches_stock_model(gpu, variant):
     """A stock transformers Llama with its attention replaced (dense chunks, then decode steps)
@@ -197,11 +223,22 @@ def _layer_qkv(attn, hidden, start, model):
     return q, k, v, qr, kr
 
 
-@pytest.mark.parametrize("selector", ["seer", "flashprefill"])
+SEER_GATES = {
+    "seer": {},  # BASELINE config 1's gate: Qavg_Kavg, both sides projected per head
+    # the reference's default gate: no query projection, W_k [Hq, 384, 128] on max/min/avg K
+    "seer_default_gate": dict(seerattn_gate_type="Qavg_Kmaxminavg", seerattn_gate_force_double=False),
+    "seer_kv_aware_gate": dict(seerattn_gate_type="Qavg_Kmaxminavg", seerattn_gate_force_double=False,
+                               seerattn_compactattn_kv_group_aware_gate=True),
+}
+
+
+@pytest.mark.parametrize("selector", ["seer", "seer_default_gate", "seer_kv_aware_gate", "flashprefill"])
 def test_layer_tables_bit_exact(gpu, selector):
     print(f"case: model layer tables {selector}", flush=True)
-    cls = SeerAttnLlamaChunkedDenseForCausalLM if selector == "seer" else SeerAttnLlamaFlashPrefillCompactAttnForCausalLM
-    m = _model(cls, gpu, qk_scale=8.0 if selector == "seer" else 40.0, gate_scale=20.0, seerattn_threshold=0.1)
+    seer = selector.startswith("seer")
+    cls = SeerAttnLlamaChunkedDenseForCausalLM if seer else SeerAttnLlamaFlashPrefillCompactAttnForCausalLM
+    m = _model(cls, gpu, qk_scale=8.0 if seer else 40.0, gate_scale=20.0, seerattn_threshold=0.1,
+               **SEER_GATES.get(selector, {}))
     layer_idx = 1
     captured, handle, attn = _capture_layer_inputs(m, layer_idx)
     ids = synthetic_prompt(1, T, m.config.vocab_size, 7, gpu)
@@ -219,12 +256,9 @@ def test_layer_tables_bit_exact(gpu, selector):
     P = [stats["past_blocks"]]
     Hkv = m.config.num_key_value_heads
     c = m.config
-    if selector == "seer":
+    if seer:
         bcos, bsin = (f32(t) for t in m.model.rotary_emb.blocks())
-        wq = f32(attn.attn_gate.mask_linear_q.weight)
-        wk = f32(attn.attn_gate.mask_linear_k.weight)
-        qhat = oracle.gate_project(oracle.block_mean(bits(q_nope)), wq, bcos, bsin, P)
-        khat = oracle.gate_project(oracle.block_mean(bits(k_nope_all)), wk, bcos, bsin, [0])
+        qhat, khat = oracle_gate_summaries(attn.attn_gate, bits(q_nope), bits(k_nope_all), bcos, bsin, P[0])
         scores = oracle.block_scores(qhat, khat, P, 128 ** -0.5)
         rule = oracle.Rule(threshold=c.seerattn_threshold, sink_blocks=c.compactattn_sink_blocks,
                            local_blocks=c.compactattn_local_blocks)

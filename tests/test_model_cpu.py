@@ -2,6 +2,7 @@
 initialisation and argument errors (no kernel runs without a GPU)."""
 from __future__ import annotations
 
+import numpy as np
 import pytest
 import torch
 
@@ -33,8 +34,13 @@ def test_config_validation():
         tiny(seerattn_gate_block_size=128).validate()
     with pytest.raises(ValueError, match="head_dim 128"):
         tiny(head_dim=64).validate()
-    with pytest.raises(ValueError, match="Qavg_Kavg"):
-        tiny(seerattn_gate_type="Qmax_Kmax").validate()
+    # every gate type of the reference validates; malformed names do not
+    tiny(seerattn_gate_type="Qmax_Kmax").validate()
+    tiny(seerattn_gate_type="Qavg_Kmaxminavg", seerattn_gate_force_double=False).validate()
+    with pytest.raises(ValueError, match="Q<pools>_K<pools>"):
+        tiny(seerattn_gate_type="avg").validate()
+    with pytest.raises(ValueError, match="unknown pooling name"):
+        tiny(seerattn_gate_type="Qavg_Kmedian").validate()
     assert SeerAttnLlamaConfig.from_dict(tiny().to_dict()) == tiny()
 
 
@@ -88,16 +94,62 @@ def test_paged_cache_decode_append_rules():
     from compactattention_amd.kv_cache import PagedKVCache
 
     c = PagedKVCache(1, 2, 192, "cpu")
-    k = torch.randn((1, 64, 2, 128)).to(torch.bfloat16)
-    c.length = 64  # as after one prefill chunk
-    start = c.append_tokens(k[:, :3], k[:, :3])
+    k = torch.randn((1, 67, 2, 128)).to(torch.bfloat16)
+    v = torch.randn((1, 67, 2, 128)).to(torch.bfloat16)
+    assert c.append_tokens(k[:, :64], v[:, :64]) == 0
+    start = c.append_tokens(k[:, 64:], v[:, 64:])
     assert start == 64 and c.length == 67
-    assert torch.equal(c.k[0, :, 64:67], k[0, :3].transpose(0, 1))
+    assert torch.equal(c.k_hf()[0], k[0].transpose(0, 1))
+    assert torch.equal(c.v_hf()[0], v[0].transpose(0, 1))
     with pytest.raises(ValueError, match="partial block"):
-        c.append(k, k)
-    with pytest.raises(ValueError, match="capacity"):
-        c.append_tokens(torch.zeros((1, 126, 2, 128), dtype=torch.bfloat16),
-                        torch.zeros((1, 126, 2, 128), dtype=torch.bfloat16))
+        c.append(k[:, :64], k[:, :64])
+
+
+def test_paged_cache_allocator_growth_fork_and_copy_on_write():
+    """Host logic of the page pool and page table (CPU tensors; the kernels only read them):
+    pages are handed out per (row, block) as the sequence grows, the pool and the page
+    table grow past their initial size without moving any stored token, forked requests
+    share pages by reference count, and a decode append into a shared partial page copies
+    it first."""
+    from compactattention_amd.kv_cache import PagedKVCache
+
+    g = torch.Generator().manual_seed(0)
+    c = PagedKVCache(2, 2, 128, "cpu", pool_pages=3)  # table for 2 blocks, 3 pages for 4 rows
+    rows = 4
+    toks = []
+    for n in (64, 64, 40, 1):  # grows through 2 -> 4 blocks of table and 3 -> 16 pages
+        k = torch.randn((2, n, 2, 128), generator=g).to(torch.bfloat16)
+        c.append_tokens(k, -k)
+        toks.append(k)
+    allk = torch.cat(toks, dim=1)
+    assert c.length == 169 and c.cap >= 3 and c.pool.num_pages >= rows * 3
+    assert torch.equal(c.k_hf(), allk.transpose(1, 2)) and torch.equal(c.v_hf(), -allk.transpose(1, 2))
+    # one distinct page per (row, block), the device table mirrors the host table
+    pt = c.page_table.numpy()
+    mapped = pt[:, :3]
+    assert (mapped >= 0).all() and len(set(mapped.ravel().tolist())) == rows * 3
+    assert (pt[:, 3:] == -1).all()
+    assert (c.pool.refs[mapped.ravel()] == 1).all()
+    # request 1 takes request 0's contents by sharing its pages
+    free_before = c.pool.free_pages
+    c.fork(0, 1)
+    assert c.pool.free_pages == free_before + 2 * 3  # request 1's own pages came back
+    assert np.array_equal(c.page_table.numpy()[2:4, :3], c.page_table.numpy()[0:2, :3])
+    assert (c.pool.refs[c.page_table.numpy()[0:2, :3].ravel()] == 2).all()
+    assert torch.equal(c.k_hf()[1], c.k_hf()[0])
+    # decode append into the shared partial block 2: copy-on-write for both requests' rows
+    k = torch.randn((2, 3, 2, 128), generator=g).to(torch.bfloat16)
+    shared_page = int(c.page_table[0, 2])
+    c.append_tokens(k, k)
+    pt = c.page_table.numpy()
+    assert pt[0, 2] != pt[2, 2] and shared_page in (pt[0, 2], pt[2, 2])
+    assert np.array_equal(pt[0:2, :2], pt[2:4, :2])  # full blocks stay shared
+    kk = c.k_hf()
+    assert torch.equal(kk[0, :, :169], allk[0].transpose(0, 1))
+    assert torch.equal(kk[1, :, :169], allk[0].transpose(0, 1))
+    assert torch.equal(kk[:, :, 169:], k.transpose(1, 2))
+    c.reset()
+    assert c.length == 0 and c.pool.free_pages == c.pool.num_pages and (c.page_table.numpy() == -1).all()
 
 
 def test_fused_projections_reseat_weights_and_fall_back():

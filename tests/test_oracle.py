@@ -408,3 +408,51 @@ def test_oracle_flashprefill_path_matches_reference_tables():
         _, _, tab, cnt = oracle.union_compact(oracle.select_rows(s, past, rule), Hkv, past, last_n)
         rtab, rcnt = ref_flashprefill_tables(s, past, Hkv, 0.4, 1, 2, k, last_n)
         assert np.array_equal(cnt, rcnt) and np.array_equal(tab, rtab), (k, last_n)
+
+
+def test_block_pool_matches_numpy():
+    """max / min pooling equal numpy's over the bf16 values exactly; avg equals block_mean;
+    the pools are concatenated max, min, avg (the reference's torch.cat order over
+    combinations of ('max', 'min', 'avg'), attn_gate.py:124-130,265-278)."""
+    x = _bf16((2, 192, 3, 128))
+    xf = oracle.bf16_bits_to_f32(x).reshape(2, 3, 64, 3, 128)  # [B, nb, 64, H, D]
+    mx = xf.max(axis=2).transpose(0, 2, 1, 3)
+    mn = xf.min(axis=2).transpose(0, 2, 1, 3)
+    avg = oracle.block_mean(x)
+    for names in (("max",), ("min",), ("avg",), ("max", "avg"), ("min", "avg"), ("max", "min", "avg")):
+        got = oracle.block_pool(x, oracle.pool_bits(names))
+        ref = np.concatenate([{"max": mx, "min": mn, "avg": avg}[n] for n in names], axis=-1)
+        assert got.shape == (2, 3, 3, 128 * len(names))
+        assert float_bits_equal_np(got, ref), names
+
+
+def float_bits_equal_np(a, b):
+    return np.array_equal(np.ascontiguousarray(a, np.float32).view(np.uint32),
+                          np.ascontiguousarray(b, np.float32).view(np.uint32))
+
+
+def test_gate_project_wide_input_matches_multiheadlinear():
+    """Projection of C*128 (and G*C*128) pooled inputs against the reference's MultiHeadLinear
+    einsum in fp64, including its repeat of K heads to the Q heads (repeat_kv_varlen,
+    modules/common.py:186-193) and the kv-group-aware query reshape (attn_gate.py:96-111)."""
+    B, Hkv, G, N = 1, 2, 3, 4
+    Hq = Hkv * G
+    C = 3
+    kp = RNG.standard_normal((B, Hkv, N, C * 128)).astype(np.float32)
+    Wk = (RNG.standard_normal((Hq, C * 128, 128)) * 0.02).astype(np.float32)
+    # K repeated to the Q heads (head hk*G + j uses KV head hk), projected per Q head
+    rep = np.repeat(kp, G, axis=1)
+    got = oracle.gate_project(rep, Wk, None, None, [0])
+    x = torch.tensor(kp, dtype=torch.float64).permute(0, 2, 1, 3)  # [B, N, Hkv, in]
+    xr = x.unsqueeze(-2).expand(B, N, Hkv, G, C * 128).reshape(B, N, Hq, C * 128)
+    ref = torch.einsum("bshi,hio->bsho", xr, torch.tensor(Wk, dtype=torch.float64)).permute(0, 2, 1, 3)
+    assert np.abs(got - ref.numpy()).max() <= 1e-5
+    # kv-group-aware query: the G heads' pooled vectors of a group concatenated head-major
+    qp = RNG.standard_normal((B, Hq, N, 128)).astype(np.float32)
+    Wq = (RNG.standard_normal((Hkv, G * 128, 128)) * 0.02).astype(np.float32)
+    cat = qp.reshape(B, Hkv, G, N, 128).transpose(0, 1, 3, 2, 4).reshape(B, Hkv, N, G * 128)
+    got = oracle.gate_project(cat, Wq, None, None, [0])
+    q = torch.tensor(qp, dtype=torch.float64).permute(0, 2, 1, 3)  # [B, N, Hq, 128]
+    grouped = q.contiguous().view(B, N, Hkv, G, 128).reshape(B, N, Hkv, G * 128)
+    ref = torch.einsum("bshi,hio->bsho", grouped, torch.tensor(Wq, dtype=torch.float64)).permute(0, 2, 1, 3)
+    assert np.abs(got - ref.numpy()).max() <= 1e-5

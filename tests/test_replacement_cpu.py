@@ -38,8 +38,13 @@ def test_replacement_structure(variant, cls):
         assert layer.self_attn.q_proj is q and layer.self_attn.o_proj is o
     keys = [k for k in r.state_dict() if k.startswith("model.layers.0.self_attn.")]
     if variant.startswith("seer"):
-        assert "model.layers.0.self_attn.attn_gate.mask_linear_q.weight" in keys
-        assert r.model.layers[0].self_attn.attn_gate.mask_linear_q.weight.dtype == torch.float32
+        # the reference's default gate (Qavg_Kmaxminavg, no force_double): no query
+        # projection, W_k per Q head over the 3 x 128 pooled K inputs
+        gate = r.model.layers[0].self_attn.attn_gate
+        assert gate.mask_linear_q is None
+        assert "model.layers.0.self_attn.attn_gate.mask_linear_k.weight" in keys
+        assert tuple(gate.mask_linear_k.weight.shape) == (4, 384, 128)
+        assert gate.mask_linear_k.weight.dtype == torch.float32
     cache = new_compactattn_cache(r, 1, 256)
     assert cache.layer(0).kgate is not None if variant.startswith("seer") else cache.layer(0).kmean is not None
     # the HIP path has no CPU fallback
@@ -73,3 +78,37 @@ def test_gate_weights_load_by_reference_key_names(tmp_path):
     with pytest.raises(ValueError, match="not in the model"):
         load_llama_attention_replacement_model(base_model=_stock(), variant="seer_compactattn",
                                                model_id=os.path.join(tmp_path, "bad.pth"))
+
+
+def test_gate_settings_from_checkpoint_config(tmp_path):
+    """The gate type, force_double and the kv-group-aware flag come from the gate checkpoint's
+    config.json, as the reference reads them with SeerAttnLlamaConfig.from_pretrained(model_id)."""
+    import json
+
+    # a Qavg_Kavg / force_double checkpoint: both projections per head, loaded by the
+    # reference's key names
+    with open(os.path.join(tmp_path, "config.json"), "w") as f:
+        json.dump({"seerattn_gate_type": "Qavg_Kavg", "seerattn_gate_force_double": True}, f)
+    gate_state = {}
+    for i in range(2):
+        gate_state[f"model.layers.{i}.self_attn.attn_gate.mask_linear_q.weight"] = torch.randn(4, 128, 128)
+        gate_state[f"model.layers.{i}.self_attn.attn_gate.mask_linear_k.weight"] = torch.randn(2, 128, 128)
+    torch.save(gate_state, os.path.join(tmp_path, "attn_gate_weights.pth"))
+    r = load_llama_attention_replacement_model(base_model=_stock(), variant="seer_compactattn", model_id=str(tmp_path))
+    assert r.compactattn_config.seerattn_gate_type == "Qavg_Kavg" and r.compactattn_config.seerattn_gate_force_double
+    got = r.state_dict()
+    for k, v in gate_state.items():
+        assert torch.equal(got[k], v)
+    cache = new_compactattn_cache(r, 1, 256)
+    assert cache.layer(0).kgate.shape[1] == 2  # gate K per KV head
+    # kv-group-aware gate (the other settings at the reference's defaults): W_q [Hkv, G*128, 128],
+    # scores per KV head
+    kv_dir = tmp_path / "kv"
+    os.makedirs(kv_dir)
+    with open(os.path.join(kv_dir, "config.json"), "w") as f:
+        json.dump({"seerattn_compactattn_kv_group_aware_gate": True}, f)
+    torch.save({}, os.path.join(kv_dir, "attn_gate_weights.pth"))
+    r = load_llama_attention_replacement_model(base_model=_stock(), variant="seer_compactattn", model_id=str(kv_dir))
+    gate = r.model.layers[0].self_attn.attn_gate
+    assert gate.kv_group_aware_query and tuple(gate.mask_linear_q.weight.shape) == (2, 2 * 128, 128)
+    assert gate.query_heads == 2 and gate.key_heads == 2

@@ -94,3 +94,33 @@ def ref_flashprefill_tables(scores, past, Hkv, alpha, sink, window, min_budget, 
             table[b * Hkv + hk, :len(ids)] = ids
             counts[b * Hkv + hk] = len(ids)
     return table, counts
+
+
+def oracle_gate_summaries(gate, q_bits, k_bits, cos, sin, q_first_block):
+    """The oracle's (qhat, khat) for an AttnGate of any type: pooling by the gate's pool sets,
+    then the reference's projection case (attn_gate.py:74-86) -- no query projection (the K
+    blocks repeated to the Q heads and projected per Q head), per-Q-head projections, or the
+    kv-group-aware query over the group's concatenated pooled heads -- and block RoPE.
+    q_bits [B, Lq, Hq, 128], k_bits [B, K, Hkv, 128] (K blocks from block 0); cos/sin fp32
+    [rows, 128] numpy tables by absolute block id."""
+    import oracle
+
+    B, _, Hq, _ = q_bits.shape
+    Hkv = k_bits.shape[2]
+    G = Hq // Hkv
+    qp = oracle.block_pool(q_bits, oracle.pool_bits(gate.q_pooling_funcs))
+    kp = oracle.block_pool(k_bits, oracle.pool_bits(gate.k_pooling_funcs))
+    first = [q_first_block] * B
+    wk = gate.mask_linear_k.weight.detach().float().cpu().numpy()
+    if gate.mask_linear_q is None:
+        eye = np.tile(np.eye(128, dtype=np.float32), (Hq, 1, 1))
+        qhat = oracle.gate_project(qp, eye, cos, sin, first)
+        kp = np.repeat(kp, G, axis=1)
+    else:
+        wq = gate.mask_linear_q.weight.detach().float().cpu().numpy()
+        if gate.kv_group_aware_query:
+            Qb, w = qp.shape[2], qp.shape[3]
+            qp = qp.reshape(B, Hkv, G, Qb, w).transpose(0, 1, 3, 2, 4).reshape(B, Hkv, Qb, G * w)
+        qhat = oracle.gate_project(qp, wq, cos, sin, first)
+    khat = oracle.gate_project(kp, wk, cos, sin, [0] * B)
+    return qhat, khat
