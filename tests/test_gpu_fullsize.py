@@ -1,14 +1,19 @@
-"""BASELINE configs at their full sizes on the GPU.  Config 2: a 131072-token paged heads-first
-cache, a 1024-token chunk, 32 Q / 8 KV heads, FlashPrefill pooled top-k (k = 10) + sink block 0
-+ 2 local blocks; config 1 (AttnGate at 32768 tokens) and config 4 (ragged batch) below.
+"""BASELINE configs at their full sizes (and config 3's attention shape) on the GPU.
 
-The selection path is integer/fp32 work with a fixed evaluation order, so at this size it is
-still checked bit for bit against the CPU oracle (which runs it in well under a second):
-block means of the whole cache, pooled queries, per-row masks, the GQA union, tables and
-counts.  The attention is checked on a sample of query tokens (the first and the last 8 of
-the chunk, every head) against the fp64-accumulated oracle over the same selected blocks,
-and through properties that hold at any size: the tables' structure, and agreement of the
-automatic split plan with the unsplit launch.
+Config 2: a 131072-token paged heads-first cache, a 1024-token chunk, 32 Q / 8 KV heads,
+FlashPrefill pooled top-k (k = 10, about a quarter of the past after the union) + sink block 0
++ 2 local blocks, and the 10 % and 50 % points of the keep sweep.  Config 0: 256 queries over
+8192 keys.  Config 1: AttnGate at 32768 tokens.  Config 3's layer shape: a 2048-token chunk
+at the end of a 131072-token prompt.  Config 4: the ragged four-request batch at G = 7.
+
+The selection path is integer/fp32 work with a fixed evaluation order, so at these sizes it
+is still checked bit for bit against the CPU oracle (which runs it in well under a second):
+block means, pooled queries, per-row masks, the GQA union, tables and counts.  The attention
+output is checked on every query row of every head against an fp32 torch attention on the
+GPU over the same selected blocks (tests/util.torch_reference_check: gathered K/V, causal
+mask, softmax, PV -- no code shared with the kernel or the oracle), at the north-star
+tolerance (max-abs 2e-2, mean-abs 2e-3), and so is the log-sum-exp; a few rows are also
+checked against the fp64 C oracle, which ties the two references together.
 """
 from __future__ import annotations
 
@@ -20,9 +25,9 @@ import torch
 
 import oracle
 from compactattention_amd import ops
-from compactattention_amd.synthetic import make_chunk_device
+from compactattention_amd.synthetic import make_chunk, make_chunk_device
 
-from .util import bits, f32, float_bits_equal, unpack_rowmask
+from .util import bits, f32, float_bits_equal, torch_reference_check, unpack_rowmask
 
 pytestmark = pytest.mark.gpu
 
@@ -30,8 +35,79 @@ PAST, LQ, HQ, HKV = 131072, 1024, 32, 8
 TOPK = 10
 ATOL_MAX = 2e-2
 ATOL_MEAN = 2e-3
+SCALE = 1.0 / math.sqrt(128)
 
 
+def _fill(ch, K, V, kmean, past: int, lq: int, step: int = 16384, **gate):
+    """The cache-fill kernel appends the past in pieces, then the chunk (the path's append)."""
+    for t0 in range(0, past, step):
+        t1 = min(past, t0 + step)
+        ops.cache_fill(ch.k[:, :, t0:t1].transpose(1, 2).contiguous(), ch.v[:, :, t0:t1].transpose(1, 2).contiguous(),
+                       K, V, [t0 // 64], ch.kv_cap, kmean, **gate)
+    ops.cache_fill(ch.k[:, :, past:past + lq].transpose(1, 2).contiguous(),
+                   ch.v[:, :, past:past + lq].transpose(1, 2).contiguous(), K, V, [past // 64], ch.kv_cap, kmean,
+                   **gate)
+
+
+def _oracle_scores(ch):
+    """Oracle pooled scores of a single-request chunk from the oracle's own block means."""
+    P = ch.past_blocks
+    nkb = P[0] + ch.q.shape[1] // 64
+    hkv = ch.k.shape[1]
+    khat_ref = oracle.block_mean(np.ascontiguousarray(bits(ch.k)[:, :, :nkb * 64].transpose(0, 2, 1, 3)))
+    khat = np.zeros((1, hkv, ch.kv_cap, 128), dtype=np.float32)
+    khat[:, :, :nkb] = khat_ref
+    qhat_ref = oracle.block_mean(bits(ch.q))
+    return khat_ref, qhat_ref, oracle.block_scores(qhat_ref, khat, P, SCALE)
+
+
+def _select(qhat, kmean, P, hkv, cap, topk):
+    rule = ops.Rule(topk=topk, sink_blocks=1, local_blocks=2)
+    rowmask, _ = ops.score_select(qhat, kmean, SCALE, rule, P, hkv, cap)
+    table, counts, _, _ = ops.union_compact(rowmask, P, hkv, cap)
+    return rowmask, table, counts
+
+
+def _keep_ratio(counts, P, qb):
+    return float((counts.float() - qb).mean().item()) / P
+
+
+def _calibrate(qhat, kmean, P, hkv, cap, qb, target):
+    """The top-k whose post-union past keep ratio is closest to target (as the bench does)."""
+    best = None
+    for k in (1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20, 24, 28, 32, 40, 48, 56, 64):
+        _, _, counts = _select(qhat, kmean, P, hkv, cap, k)
+        r = _keep_ratio(counts, P[0], qb)
+        if best is None or abs(r - target) < abs(best[1] - target):
+            best = (k, r)
+    return best
+
+
+def _check_tables(rowmask, table, counts, sc, P, hkv, cap, topk):
+    keep = oracle.select_rows(sc, P, oracle.Rule(topk=topk, sink_blocks=1, local_blocks=2))
+    assert np.array_equal(unpack_rowmask(rowmask, cap), keep)
+    _, _, ref_tab, ref_cnt = oracle.union_compact(keep, hkv, P)
+    assert np.array_equal(counts.cpu().numpy(), ref_cnt)
+    assert np.array_equal(table.cpu().numpy(), ref_tab)
+
+
+def _check_attention(q, kc, vc, P, table, counts, cap, hkv, oracle_rows=((0, 4),), **kw):
+    """All rows against the fp32 torch reference; a few rows against the fp64 C oracle."""
+    out, lse = ops.attn_fwd(q, ops.KV.heads_first(kc), ops.KV.heads_first(vc), table, counts, P, SCALE, cap, hkv,
+                            with_lse=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    torch_reference_check(out, q, kc, vc, P, table, counts, SCALE, lse=lse)
+    got = f32(out)
+    tab, cnt = table.cpu().numpy(), counts.cpu().numpy()
+    for q0, q1 in oracle_rows:
+        ref = oracle.attention(bits(q), bits(kc), bits(vc), P, tab, cnt, SCALE, q_range=(q0, q1))
+        err = np.abs(got[:, q0:q1] - ref[:, q0:q1])
+        assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (q0, err.max(), err.mean())
+    return out
+
+
+# ----------------------------------------------------------------------------- config 2
 @pytest.fixture(scope="module")
 def full(gpu):
     print("case: full-size config 2 (131072 past tokens, chunk 1024, 32/8 heads)", flush=True)
@@ -40,44 +116,25 @@ def full(gpu):
     kc, vc = torch.zeros_like(ch.k), torch.zeros_like(ch.v)
     K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
     kmean = torch.zeros((HKV, cap, 128), dtype=torch.float32, device=gpu)
-    step = 16384
-    for t0 in range(0, PAST, step):  # the past, then the chunk (the path's append)
-        t1 = min(PAST, t0 + step)
-        ops.cache_fill(ch.k[:, :, t0:t1].transpose(1, 2).contiguous(), ch.v[:, :, t0:t1].transpose(1, 2).contiguous(),
-                       K, V, [t0 // 64], cap, kmean)
-    ops.cache_fill(ch.k[:, :, PAST:PAST + LQ].transpose(1, 2).contiguous(),
-                   ch.v[:, :, PAST:PAST + LQ].transpose(1, 2).contiguous(), K, V, P, cap, kmean)
-    scale = 1.0 / math.sqrt(128)
-    rule = ops.Rule(topk=TOPK, sink_blocks=1, local_blocks=2)
+    _fill(ch, K, V, kmean, PAST, LQ)
     qhat = ops.pool_query(ch.q, P, cap)
-    rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, HKV, cap)
-    table, counts, _, _ = ops.union_compact(rowmask, P, HKV, cap)
+    rowmask, table, counts = _select(qhat, kmean, P, HKV, cap, TOPK)
     torch.cuda.synchronize()
+    khat_ref, qhat_ref, sc = _oracle_scores(ch)
     return dict(ch=ch, cap=cap, P=P, K=K, V=V, kc=kc, vc=vc, kmean=kmean, qhat=qhat, rowmask=rowmask,
-                table=table, counts=counts, scale=scale)
+                table=table, counts=counts, khat_ref=khat_ref, qhat_ref=qhat_ref, sc=sc)
 
 
 def test_fullsize_cache_and_selection_bit_exact(full):
     ch, cap, P = full["ch"], full["cap"], full["P"]
     nkb = P[0] + LQ // 64
-    kbits = bits(ch.k)  # [1, Hkv, cap*64, 128]
     # the cache holds the appended tokens unchanged
     assert torch.equal(full["kc"][:, :, :nkb * 64].view(torch.int16), ch.k[:, :, :nkb * 64].view(torch.int16))
     assert torch.equal(full["vc"][:, :, :nkb * 64].view(torch.int16), ch.v[:, :, :nkb * 64].view(torch.int16))
-    # block means of every cached block
-    khat_ref = oracle.block_mean(np.ascontiguousarray(kbits[:, :, :nkb * 64].transpose(0, 2, 1, 3)))  # [1, Hkv, nkb, 128]
-    assert float_bits_equal(f32(full["kmean"][:, :nkb]).reshape(1, HKV, nkb, 128), khat_ref)
-    # pooled queries, scores, per-row masks, union and tables
-    qhat_ref = oracle.block_mean(bits(ch.q))
-    assert float_bits_equal(f32(full["qhat"]), qhat_ref)
-    khat = np.zeros((1, HKV, cap, 128), dtype=np.float32)
-    khat[:, :, :nkb] = khat_ref
-    sc = oracle.block_scores(qhat_ref, khat, P, full["scale"])
-    keep = oracle.select_rows(sc, P, oracle.Rule(topk=TOPK, sink_blocks=1, local_blocks=2))
-    assert np.array_equal(unpack_rowmask(full["rowmask"], cap), keep)
-    _, _, ref_tab, ref_cnt = oracle.union_compact(keep, HKV, P)
-    assert np.array_equal(full["counts"].cpu().numpy(), ref_cnt)
-    assert np.array_equal(full["table"].cpu().numpy(), ref_tab)
+    # block means of every cached block, pooled queries, per-row masks, union and tables
+    assert float_bits_equal(f32(full["kmean"][:, :nkb]).reshape(1, HKV, nkb, 128), full["khat_ref"])
+    assert float_bits_equal(f32(full["qhat"]), full["qhat_ref"])
+    _check_tables(full["rowmask"], full["table"], full["counts"], full["sc"], P, HKV, cap, TOPK)
 
 
 def test_fullsize_table_structure(full):
@@ -99,32 +156,19 @@ def test_fullsize_table_structure(full):
     assert 0.15 < keep < 0.40, keep  # the planted inputs give about a quarter at k = 10
 
 
-def test_fullsize_attention_sampled_rows(full):
+def test_fullsize_attention_all_rows(full):
+    """Every query row of every head at 128K cached tokens (the automatic plan)."""
     ch, P, cap = full["ch"], full["P"], full["cap"]
-    out, lse = ops.attn_fwd(ch.q, full["K"], full["V"], full["table"], full["counts"], P, full["scale"], cap, HKV,
-                            with_lse=True)
-    torch.cuda.synchronize()
-    got, got_lse = f32(out), f32(lse)
-    assert np.isfinite(got).all()
-    qbits, kbits, vbits = bits(ch.q), bits(ch.k), bits(ch.v)
-    table, counts = full["table"].cpu().numpy(), full["counts"].cpu().numpy()
-    for q0, q1 in [(0, 8), (LQ - 8, LQ)]:
-        ref, ref_lse = oracle.attention(qbits, kbits, vbits, P, table, counts, full["scale"], with_lse=True,
-                                        q_range=(q0, q1))
-        err = np.abs(got[:, q0:q1] - ref[:, q0:q1])
-        assert err.max() <= ATOL_MAX, (q0, err.max())
-        assert err.mean() <= ATOL_MEAN, (q0, err.mean())
-        lerr = np.abs(got_lse[:, :, q0:q1] - ref_lse[:, :, q0:q1])
-        assert lerr.max() <= 4e-3, (q0, lerr.max())
+    _check_attention(ch.q, full["kc"], full["vc"], P, full["table"], full["counts"], cap, HKV,
+                     oracle_rows=((0, 4), (LQ - 4, LQ)))
 
 
 @pytest.mark.parametrize("forced", [1, 3])
 def test_fullsize_split_plan_matches_unsplit(full, forced):
-    """The automatic plan (one launch, 128-row tiles whose two key groups split each row's
-    list inside the workgroup) against forced splits of the key range through HBM partials
-    and the merge kernel."""
+    """The automatic split plan against forced split counts (1: no partials; 3: three
+    partials per row merged by LSE)."""
     ch, P, cap = full["ch"], full["P"], full["cap"]
-    args = (ch.q, full["K"], full["V"], full["table"], full["counts"], P, full["scale"], cap, HKV)
+    args = (ch.q, full["K"], full["V"], full["table"], full["counts"], P, SCALE, cap, HKV)
     auto = ops.attn_fwd(*args, num_splits=0)
     other = ops.attn_fwd(*args, num_splits=forced)
     torch.cuda.synchronize()
@@ -134,22 +178,50 @@ def test_fullsize_split_plan_matches_unsplit(full, forced):
     assert d.max().item() <= ATOL_MAX and d.mean().item() <= 2e-4, (d.max().item(), d.mean().item())
 
 
-def _check_sampled_attention(q, k, v, P, table, counts, cap, hkv, scale, samples):
-    """Attention of the sampled query tokens against the oracle over the same tables."""
-    out, lse = ops.attn_fwd(q, ops.KV.heads_first(k), ops.KV.heads_first(v), table, counts, P, scale, cap, hkv,
-                            with_lse=True)
-    torch.cuda.synchronize()
-    got, got_lse = f32(out), f32(lse)
-    assert np.isfinite(got).all()
-    qbits, kbits, vbits = bits(q), bits(k), bits(v)
+@pytest.mark.parametrize("target", [0.10, 0.50])
+def test_fullsize_keep_sweep_points(full, target):
+    """The bench's 10 % and 50 % keep points: top-k calibrated like the bench, tables bit-exact
+    against the oracle, every attention row against the fp32 torch reference."""
+    print(f"case: full-size config 2 sweep point {target}", flush=True)
+    ch, P, cap = full["ch"], full["P"], full["cap"]
+    qb = LQ // 64
+    topk, ratio = _calibrate(full["qhat"], full["kmean"], P, HKV, cap, qb, target)
+    assert abs(ratio - target) < 0.06, (topk, ratio)
+    rowmask, table, counts = _select(full["qhat"], full["kmean"], P, HKV, cap, topk)
+    _check_tables(rowmask, table, counts, full["sc"], P, HKV, cap, topk)
+    _check_attention(ch.q, full["kc"], full["vc"], P, table, counts, cap, HKV)
+
+
+# ----------------------------------------------------------------------------- config 0
+def test_config0_shape(gpu):
+    """Config 0 (BASELINE's CPU-runnable case) on the HIP path: 256 queries over 8192 keys
+    (P = 124, C = 4), 32 / 8 heads, planted inputs (seed 1234, 8 blocks per KV head get +2.0
+    along a shared direction), FlashPrefill pooled top-k + sink block 0 + 2 local blocks at
+    about 25 % post-union keep.  Tables bit-exact against the oracle, attention on every row,
+    and the planted blocks recalled by the HIP tables far above the keep ratio."""
+    print("case: config 0 (256 queries over 8192 keys, 32/8 heads)", flush=True)
+    lq, hq, hkv = 256, 32, 8
+    ch = make_chunk([8192 - lq], lq, hq, hkv, seed=1234)
+    P, cap = ch.past_blocks, ch.kv_cap
+    kc, vc = torch.zeros_like(ch.k, device=gpu), torch.zeros_like(ch.v, device=gpu)
+    K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+    kmean = torch.zeros((hkv, cap, 128), dtype=torch.float32, device=gpu)
+    dev = type(ch)(ch.q.to(gpu), ch.k.to(gpu), ch.v.to(gpu), ch.past_blocks, ch.kv_cap, ch.planted)
+    _fill(dev, K, V, kmean, P[0] * 64, lq)
+    qhat = ops.pool_query(dev.q, P, cap)
+    topk, ratio = _calibrate(qhat, kmean, P, hkv, cap, lq // 64, 0.25)
+    assert 0.2 <= ratio <= 0.3, (topk, ratio)
+    rowmask, table, counts = _select(qhat, kmean, P, hkv, cap, topk)
+    _, _, sc = _oracle_scores(ch)
+    _check_tables(rowmask, table, counts, sc, P, hkv, cap, topk)
+    _check_attention(dev.q, kc, vc, P, table, counts, cap, hkv, oracle_rows=((0, lq),))
     tab, cnt = table.cpu().numpy(), counts.cpu().numpy()
-    for q0, q1 in samples:
-        ref, ref_lse = oracle.attention(qbits, kbits, vbits, P, tab, cnt, scale, with_lse=True, q_range=(q0, q1))
-        err = np.abs(got[:, q0:q1] - ref[:, q0:q1])
-        assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (q0, err.max(), err.mean())
-        assert np.abs(got_lse[:, :, q0:q1] - ref_lse[:, :, q0:q1]).max() <= 4e-3
+    hits = sum(int(blk in set(tab[h, :cnt[h]].tolist())) for h in range(hkv) for blk in ch.planted[0][h])
+    recall = hits / sum(len(p) for p in ch.planted[0])
+    assert recall >= 0.5, (recall, ratio)
 
 
+# ----------------------------------------------------------------------------- config 1
 def test_fullsize_config1_attngate(gpu):
     """Config 1: 32768 cached tokens of which the last 1024 are the chunk (P = 496), 32 / 8
     heads, AttnGate (mean-pooled Q and K, per-head 128x128 projections ~ N(0, 0.02), block
@@ -168,17 +240,10 @@ def test_fullsize_config1_attngate(gpu):
     K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
     kmean = torch.zeros((hkv, cap, 128), dtype=torch.float32, device=gpu)
     kgate = torch.zeros_like(kmean)
-    gate = dict(gate_wk=wk.to(gpu), rope_cos=cos.to(gpu), rope_sin=sin.to(gpu), kgate=kgate)
-    for t0 in range(0, past, 16384):
-        t1 = min(past, t0 + 16384)
-        ops.cache_fill(ch.k[:, :, t0:t1].transpose(1, 2).contiguous(), ch.v[:, :, t0:t1].transpose(1, 2).contiguous(),
-                       K, V, [t0 // 64], cap, kmean, **gate)
-    ops.cache_fill(ch.k[:, :, past:past + lq].transpose(1, 2).contiguous(),
-                   ch.v[:, :, past:past + lq].transpose(1, 2).contiguous(), K, V, P, cap, kmean, **gate)
-    scale = 1.0 / math.sqrt(128)
+    _fill(ch, K, V, kmean, past, lq, gate_wk=wk.to(gpu), rope_cos=cos.to(gpu), rope_sin=sin.to(gpu), kgate=kgate)
     rule = ops.Rule(threshold=5e-3, sink_blocks=1, local_blocks=2)
     qhat = ops.pool_query(ch.q, P, cap, gate_wq=wq.to(gpu), rope_cos=cos.to(gpu), rope_sin=sin.to(gpu))
-    rowmask, _ = ops.score_select(qhat, kgate, scale, rule, P, hkv, cap)
+    rowmask, _ = ops.score_select(qhat, kgate, SCALE, rule, P, hkv, cap)
     table, counts, _, _ = ops.union_compact(rowmask, P, hkv, cap)
     torch.cuda.synchronize()
     nkb = P[0] + lq // 64
@@ -188,15 +253,40 @@ def test_fullsize_config1_attngate(gpu):
     assert float_bits_equal(f32(kgate[:, :nkb]).reshape(1, hkv, nkb, 128), khat[:, :, :nkb])
     qref = oracle.gate_project(oracle.block_mean(bits(ch.q)), f32(wq), f32(cos), f32(sin), P)
     assert float_bits_equal(f32(qhat), qref)
-    keep = oracle.select_rows(oracle.block_scores(qref, khat, P, scale), P,
+    keep = oracle.select_rows(oracle.block_scores(qref, khat, P, SCALE), P,
                               oracle.Rule(threshold=5e-3, sink_blocks=1, local_blocks=2))
     assert np.array_equal(unpack_rowmask(rowmask, cap), keep)
     _, _, ref_tab, ref_cnt = oracle.union_compact(keep, hkv, P)
     assert np.array_equal(counts.cpu().numpy(), ref_cnt)
     assert np.array_equal(table.cpu().numpy(), ref_tab)
-    _check_sampled_attention(ch.q, kc, vc, P, table, counts, cap, hkv, scale, [(0, 8), (lq - 8, lq)])
+    _check_attention(ch.q, kc, vc, P, table, counts, cap, hkv)
 
 
+# ----------------------------------------------------------------------------- config 3 layer shape
+def test_config3_layer_shape(gpu):
+    """One layer at config 3's attention shape: the last 2048-token chunk of a 131072-token
+    prompt (P = 2016 past blocks), 32 / 8 heads, about a quarter of the past kept.  Its 256 row
+    tiles fill the CUs, so the plan runs unsplit (no partials, no merge); tables bit-exact,
+    every attention row against the fp32 torch reference."""
+    print("case: config 3 layer shape (chunk 2048 at the end of 131072 tokens, 32/8 heads)", flush=True)
+    lq = 2048
+    past = 131072 - lq
+    ch = make_chunk_device(past, lq, HQ, HKV, gpu, seed=77)
+    cap, P = ch.kv_cap, ch.past_blocks
+    assert ops.attn_pick_splits(P, lq, HQ, HKV, cap) == 1
+    kc, vc = torch.zeros_like(ch.k), torch.zeros_like(ch.v)
+    K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+    kmean = torch.zeros((HKV, cap, 128), dtype=torch.float32, device=gpu)
+    _fill(ch, K, V, kmean, past, lq)
+    qhat = ops.pool_query(ch.q, P, cap)
+    topk, ratio = _calibrate(qhat, kmean, P, HKV, cap, lq // 64, 0.25)
+    rowmask, table, counts = _select(qhat, kmean, P, HKV, cap, topk)
+    _, _, sc = _oracle_scores(ch)
+    _check_tables(rowmask, table, counts, sc, P, HKV, cap, topk)
+    _check_attention(ch.q, kc, vc, P, table, counts, cap, HKV, oracle_rows=((lq - 2, lq),))
+
+
+# ----------------------------------------------------------------------------- config 4
 def test_fullsize_config4_ragged(gpu):
     """Config 4: four requests with cached pasts 16384 / 49152 / 98304 / 131072 tokens, a
     512-token chunk each in one launch per kernel, 28 / 4 heads (G = 7), FlashPrefill pooled
@@ -215,10 +305,9 @@ def test_fullsize_config4_ragged(gpu):
     for b in range(B):
         ops.cache_fill(k[b:b + 1, :, :(P[b] + qb) * 64].transpose(1, 2).contiguous(), None, None, None, [0], cap,
                        kmean[b * hkv:(b + 1) * hkv])
-    scale = 1.0 / math.sqrt(128)
     rule = ops.Rule(topk=3, sink_blocks=1, local_blocks=2)
     qhat = ops.pool_query(q, P, cap)
-    rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, hkv, cap)
+    rowmask, _ = ops.score_select(qhat, kmean, SCALE, rule, P, hkv, cap)
     table, counts, _, _ = ops.union_compact(rowmask, P, hkv, cap)
     torch.cuda.synchronize()
     kbits = bits(k)
@@ -229,7 +318,7 @@ def test_fullsize_config4_ragged(gpu):
     assert float_bits_equal(f32(kmean).reshape(B, hkv, cap, 128), khat)
     qref = oracle.block_mean(bits(q))
     assert float_bits_equal(f32(qhat), qref)
-    keep = oracle.select_rows(oracle.block_scores(qref, khat, P, scale), P,
+    keep = oracle.select_rows(oracle.block_scores(qref, khat, P, SCALE), P,
                               oracle.Rule(topk=3, sink_blocks=1, local_blocks=2))
     assert np.array_equal(unpack_rowmask(rowmask, cap), keep)
     _, _, ref_tab, ref_cnt = oracle.union_compact(keep, hkv, P)
@@ -237,4 +326,4 @@ def test_fullsize_config4_ragged(gpu):
     assert np.array_equal(table.cpu().numpy(), ref_tab)
     kept = [float(((counts.cpu().view(B, hkv)[b] - qb).float() / P[b]).mean()) for b in range(B)]
     assert all(0.05 < r < 0.5 for r in kept), kept
-    _check_sampled_attention(q, k, v, P, table, counts, cap, hkv, scale, [(0, 4), (lq - 4, lq)])
+    _check_attention(q, k, v, P, table, counts, cap, hkv, oracle_rows=((0, 2), (lq - 2, lq)))

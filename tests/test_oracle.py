@@ -456,3 +456,31 @@ def test_gate_project_wide_input_matches_multiheadlinear():
     grouped = q.contiguous().view(B, N, Hkv, G, 128).reshape(B, N, Hkv, G * 128)
     ref = torch.einsum("bshi,hio->bsho", grouped, torch.tensor(Wq, dtype=torch.float64)).permute(0, 2, 1, 3)
     assert np.abs(got - ref.numpy()).max() <= 1e-5
+
+
+def test_torch_restatement_matches_oracle():
+    """The fp32 torch restatement timed as the CPU baseline (oracle/torch_ref.py) selects the
+    oracle's tables and attends within fp32 rounding of the fp64 oracle."""
+    from compactattention_amd.synthetic import make_chunk
+    from oracle import torch_ref
+
+    Hq, Hkv, Lq, past = 8, 2, 128, 64 * 12
+    ch = make_chunk([past], Lq, Hq, Hkv, seed=21)
+    P = ch.past_blocks[0]
+    k, v = ch.k.float(), ch.v.float()  # [1, Hkv, cap*64, D]
+    k_new = k[:, :, past:past + Lq].transpose(1, 2)
+    v_new = v[:, :, past:past + Lq].transpose(1, 2)
+    kmean_past = torch_ref.block_means(k[:, :, :past].transpose(1, 2))
+    out, k_all, v_all, _, tables = torch_ref.chunk_step(ch.q.float(), k[:, :, :past], v[:, :, :past], k_new, v_new,
+                                                         kmean_past, topk=3)
+    qb = ch.q.view(torch.int16).numpy().view(np.uint16)
+    kb = ch.k.view(torch.int16).numpy().view(np.uint16)
+    vb = ch.v.view(torch.int16).numpy().view(np.uint16)
+    khat = oracle.block_mean(np.ascontiguousarray(kb.transpose(0, 2, 1, 3)))
+    sc = oracle.block_scores(oracle.block_mean(qb), khat, [P], 1 / math.sqrt(128))
+    keep = oracle.select_rows(sc, [P], oracle.Rule(topk=3, sink_blocks=1, local_blocks=2))
+    _, _, tab, cnt = oracle.union_compact(keep, Hkv, [P])
+    for r in range(Hkv):
+        assert tables[r].tolist() == tab[r, :cnt[r]].tolist()
+    ref = oracle.attention(qb, kb, vb, [P], tab, cnt, 1 / math.sqrt(128))
+    assert np.abs(out.numpy() - ref).max() <= 1e-4

@@ -124,3 +124,49 @@ def oracle_gate_summaries(gate, q_bits, k_bits, cos, sin, q_first_block):
         qhat = oracle.gate_project(qp, wq, cos, sin, first)
     khat = oracle.gate_project(kp, wk, cos, sin, [0] * B)
     return qhat, khat
+
+
+def torch_reference_check(out, q, k_hf, v_hf, past_blocks, table, counts, scale, lse=None, atol_max=2e-2,
+                          atol_mean=2e-3, lse_atol=4e-3):
+    """Every query row of ``out`` ([B, Lq, Hq, 128] bf16, on the GPU) against an fp32 torch
+    attention on the GPU over the blocks its KV row's table lists: gather those 64-token blocks
+    of K and V, s = q k^T * scale where key position <= query position (the chunk's token t
+    sits at 64 * past_blocks[b] + t), softmax, times V.  An independent reference (torch's
+    fp32 GEMMs and softmax, no code shared with the kernel or the C oracle).  Checks the
+    north-star tolerance over all rows and, if given, the log-sum-exp ``lse`` [B, Hq, Lq].
+    Returns (max-abs, mean-abs)."""
+    B, Lq, Hq, D = q.shape
+    Hkv = k_hf.shape[1]
+    G = Hq // Hkv
+    dev = q.device
+    tab = table.detach().cpu()
+    cnt = counts.detach().cpu()
+    worst, total, n = 0.0, 0.0, 0
+    lse_worst = 0.0
+    ar = torch.arange(64, device=dev)
+    for b in range(B):
+        qpos = (64 * int(past_blocks[b]) + torch.arange(Lq, device=dev)).repeat_interleave(G)  # rows t*G + g
+        for hk in range(Hkv):
+            r = b * Hkv + hk
+            ids = tab[r, :int(cnt[r])].to(dev).long()
+            keys = (ids[:, None] * 64 + ar[None, :]).reshape(-1)
+            kf = k_hf[b, hk].index_select(0, keys).float()
+            vf = v_hf[b, hk].index_select(0, keys).float()
+            qf = q[b, :, hk * G:(hk + 1) * G].float().reshape(Lq * G, D)
+            s = (qf @ kf.T.contiguous()) * scale
+            s.masked_fill_(keys[None, :] > qpos[:, None], float("-inf"))
+            ref_lse = torch.logsumexp(s, dim=-1)
+            o = torch.softmax(s, dim=-1) @ vf
+            del s
+            got = out[b, :, hk * G:(hk + 1) * G].float().reshape(Lq * G, D)
+            err = (got - o).abs()
+            worst = max(worst, err.max().item())
+            total += err.sum().item()
+            n += err.numel()
+            if lse is not None:
+                got_lse = lse[b, hk * G:(hk + 1) * G].float().transpose(0, 1).reshape(-1)
+                lse_worst = max(lse_worst, (got_lse - ref_lse).abs().max().item())
+    mean = total / n
+    assert worst <= atol_max and mean <= atol_mean, (worst, mean)
+    assert lse_worst <= lse_atol, lse_worst
+    return worst, mean
