@@ -151,12 +151,12 @@ class PagedKVCache:
         self._grow_cap(b1)
         need = self._pt[:, b0:b1] < 0
         n = int(need.sum())
-        if n:
+        if n:  # only new pages touch the device table (a small upload on the current stream)
             pages = np.asarray(self.pool.alloc(n), np.int32)
             block = self._pt[:, b0:b1]
             block[need] = pages  # row-major: a row's new blocks get ascending page ids
             self._pt[:, b0:b1] = block
-        self._upload(b0, b1)
+            self._upload(b0, b1)
 
     def reserve(self, tokens: int) -> None:
         """Map pages for the first ``tokens`` tokens of every request ahead of time."""
@@ -268,11 +268,22 @@ class PagedKVCache:
     def v_hf(self) -> torch.Tensor:
         return self._gather(self.pool.v)
 
-    def reset(self) -> None:
-        """Drop every request's pages (the pool keeps its size)."""
-        mapped = self._pt[self._pt >= 0]
-        if mapped.size:
-            self.pool.release(mapped)
-        self._pt[:] = -1
-        self.page_table.fill_(-1)
+    def reset(self, keep_pages: bool = False) -> None:
+        """Empty the cache.  By default every request's pages go back to the pool (which keeps
+        its size); with keep_pages the pages a row owns alone stay mapped for the next
+        sequence (no allocation or page-table upload when it refills them), while pages
+        shared with another request are released so a refill never writes into them."""
+        if keep_pages:
+            mapped = self._pt >= 0
+            shared = mapped & (self.pool.refs[np.where(mapped, self._pt, 0)] > 1)
+            if shared.any():
+                self.pool.release(self._pt[shared])
+                self._pt[shared] = -1
+                self._upload(0, self.cap)
+        else:
+            mapped = self._pt[self._pt >= 0]
+            if mapped.size:
+                self.pool.release(mapped)
+            self._pt[:] = -1
+            self.page_table.fill_(-1)
         self.length = 0

@@ -228,6 +228,10 @@ class ChunkedPrefillCache:
                          with_kgate=with_kgate, kgate_heads=kgate_heads)
             for _ in range(config.num_hidden_layers)
         ]
+        # pages for max_tokens up front, so a prefill of that length maps nothing on the way;
+        # a longer sequence grows the pool and the page tables on demand
+        for layer in self.layers:
+            layer.reserve(max_tokens)
 
     def layer(self, idx: int) -> PagedKVCache:
         return self.layers[idx]
@@ -236,8 +240,9 @@ class ChunkedPrefillCache:
         return self.layers[0].length
 
     def reset(self) -> None:
+        """Start a new sequence in the same pages (pages shared by a fork are released)."""
         for c in self.layers:
-            c.reset()
+            c.reset(keep_pages=True)
 
 
 class CompactAttnLlamaDecoderLayer(nn.Module):

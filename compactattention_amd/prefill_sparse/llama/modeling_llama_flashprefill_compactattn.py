@@ -49,6 +49,7 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
         self.qkv = FusedProjections(self, ("q_proj", "k_proj", "v_proj"))
         self.attention_timer: Optional[list] = None  # a list collects timing events of the attention core
+        self.table_sink: Optional[list] = None  # a list collects (counts, chunk length, past blocks) per call
         self.compactattn_version = COMPACTATTN_VERSION
         self.compactattn_debug = False
         self._compactattn_last_stats = None
@@ -95,6 +96,8 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
             K, V = cache.layouts()
             out = ops.attn_fwd(query_states, K, V, table, counts, P, self.scaling, cache.cap,
                                self.num_key_value_heads)
+        if self.table_sink is not None:  # per-chunk block counts (device tensors), for FLOP accounting
+            self.table_sink.append((counts, L, past))
         out = self.o_proj(out.reshape(B, L, -1))
         if self.compactattn_debug:
             self._compactattn_last_stats = {

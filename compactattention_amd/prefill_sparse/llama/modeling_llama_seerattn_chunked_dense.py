@@ -56,6 +56,7 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, config.hidden_size, **kw)
         self.qkv = FusedProjections(self, ("q_proj", "k_proj", "v_proj"))
         self.attention_timer: Optional[list] = None  # a list collects timing events of the attention core
+        self.table_sink: Optional[list] = None  # a list collects (counts, chunk length, past blocks) per call
         self.attn_gate = ATTNGATE_CLASSES[config.seerattn_gate_type](
             config.seerattn_gate_block_size, self.head_dim, config.seerattn_gate_hidden_size,
             num_k_head=self.num_key_value_heads, num_q_head=self.num_heads,
@@ -132,6 +133,8 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
             dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
             out, table, counts = self._do_chunked_compactattn_attention(query_states, q, cache, past,
                                                                        block_position_embeddings, dense)
+        if self.table_sink is not None:  # per-chunk block counts (device tensors), for FLOP accounting
+            self.table_sink.append((counts, L, past))
         out = self.o_proj(out.reshape(B, L, -1))
         if self.compactattn_debug:
             self._compactattn_last_stats = {

@@ -134,6 +134,29 @@ def test_decode_steps_match_fp32_reference(gpu, cls):
 
 
 @pytest.mark.parametrize("cls", [SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaFlashPrefillCompactAttnForCausalLM])
+def test_paged_cache_growth_matches_reserved_cache(gpu, cls):
+    """A selecting prefill into a cache reserved for 128 tokens (the page pool, the page tables
+    and the summaries grow during the run, pages land wherever the allocator puts them) gives
+    the same logits bit for bit as one into a cache reserved for the whole prompt, and the
+    page tables are not the identity."""
+    print(f"case: model cache growth {cls.__name__}", flush=True)
+    m = _model(cls, gpu, qk_scale=8.0, gate_scale=20.0, seerattn_threshold=0.1)
+    ids = synthetic_prompt(1, T, m.config.vocab_size, 5150, gpu)
+    big = m.new_cache(1, T)
+    small = m.new_cache(1, 128)
+    pool0 = small.layer(0).pool.num_pages
+    a, _ = run_chunked_prefill_once(m, ids, CHUNK, big)
+    b, _ = run_chunked_prefill_once(m, ids, CHUNK, small)
+    assert torch.equal(a, b)
+    lay = small.layer(1)
+    assert lay.pool.num_pages > pool0 and lay.cap >= T // 64
+    pt = lay.page_table[:, :T // 64].cpu()
+    ident = torch.arange(T // 64, dtype=torch.int32)[None, :] + (T // 64) * torch.arange(pt.shape[0])[:, None]
+    assert (pt >= 0).all() and not torch.equal(pt, ident.to(torch.int32))
+    assert torch.equal(lay.k_hf(), big.layer(1).k_hf())
+
+
+@pytest.mark.parametrize("cls", [SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaFlashPrefillCompactAttnForCausalLM])
 def test_unaligned_prompt_matches_fp32_reference(gpu, cls):
     """A prompt of 64*n + 37 tokens: the last chunk's aligned part takes the chunk path and its
     37-token tail one dense decode step; the last logits match the fp32 CPU forward, a decode

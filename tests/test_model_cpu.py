@@ -187,3 +187,20 @@ def test_fused_projections_reseat_weights_and_fall_back():
     owner.to(torch.float64)
     assert not fused.intact()
     assert fused(x.double())[0].dtype == torch.float64
+
+
+def test_paged_cache_reset_keeps_owned_pages():
+    from compactattention_amd.kv_cache import PagedKVCache
+
+    c = PagedKVCache(2, 1, 128, "cpu")
+    c.reserve(128)
+    k = torch.zeros((2, 70, 1, 128), dtype=torch.bfloat16)
+    c.append_tokens(k, k)
+    owned = c.page_table.numpy().copy()
+    c.reset(keep_pages=True)
+    assert c.length == 0 and np.array_equal(c.page_table.numpy(), owned)
+    c.append_tokens(k, k)
+    c.fork(0, 1)  # request 1 now shares request 0's two pages
+    c.reset(keep_pages=True)
+    pt = c.page_table.numpy()
+    assert (pt == -1).all() and c.pool.free_pages == c.pool.num_pages  # the shared pages went back
