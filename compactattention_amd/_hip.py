@@ -19,6 +19,7 @@ ABI_VERSION = 2
 HEAD_DIM = 128
 BLOCK = 64
 MAX_BATCH = 64
+STATIC_SCRATCH_BYTES = 48 << 20
 
 CA_OK = 0
 CA_ERR_INVALID = -1
@@ -51,6 +52,7 @@ EXPORTED = (
     "ca_attn_fwd",
     "ca_attn_workspace_size",
     "ca_attn_pick_splits",
+    "ca_attn_fwd_noalloc",
     "ca_attn_decode",
     "ca_attn_decode_workspace_size",
     "ca_rope_apply",
@@ -138,6 +140,8 @@ _SIGNATURES = {
                                    _f32, _P(SeqLayout), _vp, _i32, _vp, _i64, _vp]),
     "ca_attn_workspace_size": (ctypes.c_int64, [_P(Dims), _vp, _i32]),
     "ca_attn_pick_splits": (ctypes.c_int32, [_P(Dims), _vp]),
+    "ca_attn_fwd_noalloc": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(KvLayout), _P(KvLayout), _vp, _i64, _vp,
+                                           _vp, _f32, _P(SeqLayout), _vp, _i32, _vp]),
     "ca_attn_decode": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(KvLayout), _P(KvLayout), _vp, _f32,
                                       _P(SeqLayout), _vp, _i32, _vp, _i64, _vp]),
     "ca_attn_decode_workspace_size": (ctypes.c_int64, [_P(Dims), _vp, _i32]),

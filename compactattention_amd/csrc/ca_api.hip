@@ -7,6 +7,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/compactattn.h"
@@ -188,6 +189,44 @@ int check_rule(const ca_select_rule* r) {
 }
 
 constexpr size_t kMaxLds = 160 * 1024 - 4096;  // dynamic LDS budget next to static arrays
+
+// ---- scratch of the allocation-free entry point (ca_attn_fwd_noalloc) ----
+// The split partials live in this file-scope device array: every GPU the library runs on
+// holds its own copy until the process ends.  In host code the name is only a host-side
+// handle; the array's address on a device comes from hipGetSymbolAddress with that device
+// current, looked up once per device and kept here.  Every call on a GPU shares its array
+// (calls that overlap on one GPU race); the attention kernel writes every partial row the
+// merge reads, so nothing needs clearing between calls.
+static __device__ __align__(256) uint8_t scratch[CA_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The scratch array's address on the device of `stream` (the current device, which must be
+// the stream's device).
+int scratch_for_stream(hipStream_t stream, void** ptr) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (stream != nullptr) {
+        hipDevice_t sdev = 0;
+        e = hipStreamGetDevice(stream, &sdev);
+        if (e != hipSuccess) return hip_fail(e, "hipStreamGetDevice");
+        if (sdev != dev)
+            return fail(CA_ERR_INVALID, "the stream belongs to device %d but device %d is current", (int)sdev, dev);
+    }
+    if (dev < 0 || dev >= kMaxDevices) return fail(CA_ERR_LIMIT, "device %d beyond the %d supported", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[dev] = p;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return CA_OK;
+}
 
 }  // namespace
 
@@ -464,6 +503,33 @@ int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout*
     hipError_t e = ca::launch_attn(a, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "attn launch");
     return ok();
+}
+
+int ca_attn_fwd_noalloc(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout* k,
+                        const ca_kv_layout* v, const int32_t* table, int64_t table_stride,
+                        const int32_t* counts, const int32_t* past_blocks_host, float scale,
+                        const ca_seq_layout* out, float* lse, int32_t num_splits, void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    if (num_splits < 0 || num_splits > ca::kMaxPrefillSplits)
+        return fail(CA_ERR_INVALID, "num_splits=%d outside [0, %d]", num_splits, ca::kMaxPrefillSplits);
+    int splits = num_splits;
+    if (splits == 0) {
+        // the automatic count, lowered until its partials fit the library's scratch array
+        splits = ca::attn_pick_splits(s, pb, nullptr);
+        while (splits > 1 && ca::attn_workspace_bytes(s, splits) > (int64_t)CA_STATIC_SCRATCH_BYTES) --splits;
+    }
+    const int64_t need = ca::attn_workspace_bytes(s, splits);
+    if (need > (int64_t)CA_STATIC_SCRATCH_BYTES)
+        return fail(CA_ERR_LIMIT, "num_splits=%d needs %lld bytes of split partials; the allocation-free entry "
+                    "holds at most %lld (CA_STATIC_SCRATCH_BYTES)", splits, (long long)need,
+                    (long long)CA_STATIC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    if (need > 0 && (rc = scratch_for_stream(static_cast<hipStream_t>(stream), &ws)) != CA_OK) return rc;
+    return ca_attn_fwd(dims, q, k, v, table, table_stride, counts, past_blocks_host, scale, out, lse, splits, ws,
+                       need, stream);
 }
 
 int64_t ca_attn_decode_workspace_size(const ca_dims* dims, const int32_t* kv_len_host, int32_t num_splits) {

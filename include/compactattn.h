@@ -275,6 +275,23 @@ int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout*
                 const ca_seq_layout* out, float* lse, int32_t num_splits, void* workspace,
                 int64_t workspace_bytes, void* stream);
 
+/*
+ * ca_attn_fwd without any allocation: no workspace argument, no hipMalloc/hipFree or allocating
+ * library call.  No counterpart in the reference; it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
+ * The split partials live in a library-owned device array of CA_STATIC_SCRATCH_BYTES that
+ * each GPU the library runs on holds until the process ends (looked up on a device's first
+ * call; the current device must be the stream's).  num_splits = 0 takes ca_attn_fwd's
+ * automatic count lowered until its partials fit; a positive count whose partials
+ * (ca_attn_workspace_size) exceed the array fails with CA_ERR_LIMIT.  All calls on one GPU
+ * share its array: calls that overlap on one GPU (other streams, other threads) race.
+ */
+#define CA_STATIC_SCRATCH_BYTES (48u << 20)
+int ca_attn_fwd_noalloc(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout* k,
+                        const ca_kv_layout* v, const int32_t* table, int64_t table_stride,
+                        const int32_t* counts, const int32_t* past_blocks_host, float scale,
+                        const ca_seq_layout* out, float* lse, int32_t num_splits, void* stream);
+
 /* Workspace bytes ca_attn_fwd needs for num_splits (0 = the automatic count). */
 int64_t ca_attn_workspace_size(const ca_dims* dims, const int32_t* past_blocks_host,
                                int32_t num_splits);
