@@ -256,6 +256,11 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
  * keys of the blocks table[row][0..counts[row]) of row = b*Hkv + h/G with bottom-right
  * causal masking (key position j visible iff j <= 64*P_b + t).  out has q's layout;
  * lse (optional, [B, Hq, q_len] fp32, natural log) receives the log-sum-exp.
+ * Each table row must hold strictly ascending block ids (no duplicates), as
+ * ca_union_compact, ca_compact_keep_kv and ca_dense_table write them: the kernel drops
+ * the trailing blocks past a query tile's causal edge and applies the causal mask only to
+ * the trailing run of blocks that reach past the tile's first query, so an out-of-order
+ * row could let a query see later keys.
  * num_splits >= 1 splits every row's block list that many ways; num_splits = 0 picks one
  * count for the launch (ca_attn_pick_splits) with at least ~16 blocks per split: about 256
  * work items (row tiles x splits, one per CU) when all requests have one length, 1 when
