@@ -677,6 +677,294 @@ __global__ __launch_bounds__(kSelThreads) void row_select_kernel(SelectParams p)
     }
 }
 
+// The same row selection with the row held in registers, for rows of at most 256 * NR
+// blocks: thread t owns blocks kb = t + 256 i (i < NR), which is also lane (kb % 64) of
+// wave (kb / 64) % 4 in mask chunk kb / 64, so the masks come straight from registers.
+//  - one round of global loads for the whole row;
+//  - the softmax sum keeps the order above (wave 0 over the exponentials staged in LDS);
+//  - every wave derives the top-k bound and the final cut itself from the shared lane
+//    maxima and candidate list, which saves the broadcast barriers;
+//  - the row is also staged in LDS for the whole-row search when the candidate list
+//    overflows.
+// Results are bit-identical to row_select_kernel.
+template <bool kCompute, int NR>
+__global__ __launch_bounds__(kSelThreads) void row_select_reg_kernel(SelectParams p) {
+    extern __shared__ float row[];  // [cap]
+    __shared__ float red_f[kSelWaves];
+    __shared__ float red_sum;  // its own slot: the statistics below reuse red_f without a barrier
+    __shared__ int red_i[kSelWaves];
+    __shared__ int red_z[kSelWaves];
+    __shared__ uint32_t tmax[kSelThreads];
+    __shared__ uint32_t cand_key[kCandCap];
+    __shared__ int cand_id[kCandCap];
+    __shared__ int cand_n;
+    __shared__ uint32_t sel_T;
+    __shared__ int sel_cut;
+    const Shape& s = p.s;
+    const int rid = blockIdx.x;  // (b*Hq + h)*Qb + qb
+    const int qb = rid % s.Qb;
+    const int bh = rid / s.Qb;
+    const int b = bh / s.Hq;
+    const int h = bh - b * s.Hq;
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int P = p.pb.p[b];
+    const int qabs = P + qb;
+    const int n = qabs + 1;
+    const int cap = s.cap;
+    constexpr float kNegInf = -__builtin_inff();
+
+    float v[NR];  // logits, then probabilities (compute mode); caller scores (select mode)
+    if (kCompute) {
+        float* srow = p.scores + (int64_t)rid * cap;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int kb = t + kSelThreads * i;
+            v[i] = kb < n ? srow[kb] : kNegInf;
+        }
+        float m = kNegInf;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) m = fmaxf(m, v[i]);
+        m = wave_max(m);
+        if (lane == 0) red_f[wave] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int kb = t + kSelThreads * i;
+            if (kb < n) {
+                v[i] = exp_fixed(v[i] - m);
+                row[kb] = v[i];
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // lane l sums kb = l, l + 64, ... in ascending order, then the fixed tree
+            float part = 0.0f;
+            for (int base = 0; base < n; base += 8 * 64) {
+                float e[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const int kb = base + lane + 64 * i;
+                    e[i] = kb < n ? row[kb] : 0.0f;
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    if (base + lane + 64 * i < n) part = part + e[i];
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) part = part + __shfl_down(part, o, 64);
+            if (lane == 0) red_sum = part;
+        }
+        __syncthreads();
+        const float sum = red_sum;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int kb = t + kSelThreads * i;
+            float pv = 0.0f;
+            if (kb < n) {
+                pv = v[i] / sum;
+                row[kb] = pv;
+            }
+            v[i] = pv;
+            if (kb < cap) srow[kb] = pv;
+        }
+    } else {
+        const int64_t off = b * p.ssb + h * p.ssh + qb * p.ssq;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int kb = t + kSelThreads * i;
+            v[i] = 0.0f;
+            if (kb < n) {
+                if (p.dtype == 0)
+                    v[i] = static_cast<const float*>(p.scores_in)[off + kb];
+                else
+                    v[i] = bf16_to_f32(static_cast<const uint16_t*>(p.scores_in)[off + kb]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int kb = t + kSelThreads * i;
+            if (kb < n) row[kb] = v[i];
+        }
+    }
+
+    // Row statistics as in row_select_kernel: the zeroed row's max over all Kb columns,
+    // the top-k candidate count and each thread's largest candidate key.
+    const ca_select_rule& rule = p.rule;
+    const int Kb = P + s.Qb;
+    const bool all_cols = (rule.flags & CA_RULE_TOPK_ALLCOLS) != 0;
+    const int kend = all_cols ? Kb : P;
+    const bool use_topk = (rule.flags & CA_RULE_TOPK) && rule.topk > 0 && kend > 0;
+    // candidate value of register i (block kb): the zeroed value over all columns, or a
+    // finite past score
+    auto cand_val = [&](int i, int kb, float& cv) -> bool {
+        if (all_cols) {
+            cv = kb < n ? v[i] : 0.0f;
+            if (!is_finite_f(cv)) cv = 0.0f;
+            return true;
+        }
+        cv = v[i];
+        return is_finite_f(cv);
+    };
+    {
+        float mx = kNegInf;
+        int nc = 0, nz = 0;
+        uint32_t kmax = 0;
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int kb = t + kSelThreads * i;
+            if (kb < n) {
+                if (is_finite_f(v[i]))
+                    mx = fmaxf(mx, v[i]);
+                else
+                    ++nz;
+            }
+            float cv;
+            if (use_topk && kb < kend && cand_val(i, kb, cv)) {
+                ++nc;
+                kmax = max(kmax, order_key(cv));
+            }
+        }
+        mx = wave_max(mx);
+        nc = wave_sum_int(nc);
+        nz = wave_sum_int(nz);
+        tmax[t] = kmax;
+        if (lane == 0) {
+            red_f[wave] = mx;
+            red_i[wave] = nc;
+            red_z[wave] = nz;
+        }
+        if (t == 0) cand_n = 0;
+    }
+    __syncthreads();
+    float rowmax = fmaxf(fmaxf(red_f[0], red_f[1]), fmaxf(red_f[2], red_f[3]));
+    if (n < Kb || red_z[0] + red_z[1] + red_z[2] + red_z[3] > 0) rowmax = fmaxf(rowmax, 0.0f);
+    const int ncand = red_i[0] + red_i[1] + red_i[2] + red_i[3];
+    const float alpha_cut = rule.alpha * rowmax;
+    const bool take_all = use_topk && rule.topk >= ncand;
+    const bool cut = use_topk && !take_all;
+    const int k = rule.topk;
+
+    uint32_t T = 0u;
+    int eq_cut = -1;
+    if (cut) {
+        // every wave computes the same lower bound from the 64 lane maxima
+        uint32_t lo = 0;
+        if (k <= 64) {
+            const uint32_t m1[1] = {max(max(tmax[lane], tmax[lane + 64]), max(tmax[lane + 128], tmax[lane + 192]))};
+            lo = wave_kth_largest<1>(m1, k);
+        }
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+            const int kb = t + kSelThreads * i;
+            float cv;
+            if (kb < kend && cand_val(i, kb, cv)) {
+                const uint32_t key = order_key(cv);
+                if (key >= lo) {
+                    const int slot = atomicAdd(&cand_n, 1);
+                    if (slot < kCandCap) {
+                        cand_key[slot] = key;
+                        cand_id[slot] = kb;
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        const int nl = cand_n;
+        if (nl <= 64) {
+            select_candidates<1>(cand_key, cand_id, nl, lane, k, T, eq_cut);  // every wave, same result
+        } else if (nl <= kCandCap) {
+            select_candidates<kCandSlots>(cand_key, cand_id, nl, lane, k, T, eq_cut);
+        } else {
+            // heavy ties or k > 64: wave 0 searches the staged row, as row_select_kernel does
+            if (wave == 0) {
+                auto row_val = [&](int kb, float& cv) -> bool {
+                    if (all_cols) {
+                        cv = kb < n ? row[kb] : 0.0f;
+                        if (!is_finite_f(cv)) cv = 0.0f;
+                        return true;
+                    }
+                    cv = row[kb];
+                    return is_finite_f(cv);
+                };
+                uint32_t Tw = 0;
+                for (int bit = 31; bit >= 0; --bit) {
+                    const uint32_t c = Tw | (1u << bit);
+                    int cnt = 0;
+                    for (int kb = lane; kb < kend; kb += 64) {
+                        float cv;
+                        cnt += (row_val(kb, cv) && order_key(cv) >= c) ? 1 : 0;
+                    }
+                    if (wave_sum_int(cnt) >= k) Tw = c;
+                }
+                int gt = 0;
+                for (int kb = lane; kb < kend; kb += 64) {
+                    float cv;
+                    gt += (row_val(kb, cv) && order_key(cv) > Tw) ? 1 : 0;
+                }
+                const int krem = k - wave_sum_int(gt);
+                const uint64_t lt_mask = (1ull << lane) - 1ull;
+                int seen = 0;
+                int cutw = kend;
+                for (int base = 0; base < kend; base += 64) {
+                    const int kb = base + lane;
+                    float cv = 0.0f;
+                    const bool e = kb < kend && row_val(kb, cv) && order_key(cv) == Tw;
+                    const uint64_t bal = __ballot(e);
+                    const int cnt = __popcll(bal);
+                    if (seen + cnt >= krem) {
+                        const uint64_t who = __ballot(e && seen + __popcll(bal & lt_mask) == krem - 1);
+                        cutw = base + __ffsll(static_cast<unsigned long long>(who)) - 1;
+                        break;
+                    }
+                    seen += cnt;
+                }
+                if (lane == 0) {
+                    sel_T = Tw;
+                    sel_cut = cutw;
+                }
+            }
+            __syncthreads();
+            T = sel_T;
+            eq_cut = sel_cut;
+        }
+    }
+
+    // masks: register i of this thread is lane `lane` of chunk c = wave + 4 i
+    uint32_t* out = p.rowmask + (int64_t)rid * s.words;
+    const int chunks = (s.words + 1) / 2;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int c = wave + kSelWaves * i;
+        if (c >= chunks) break;
+        const int kb = c * 64 + lane;
+        bool keep = false;
+        if (kb < n) {
+            const float x = v[i];
+            const bool fin = is_finite_f(x);
+            if ((rule.flags & CA_RULE_ALPHA) && fin && x >= alpha_cut) keep = true;
+            if ((rule.flags & CA_RULE_THRESHOLD) && x > rule.threshold) keep = true;
+            if (kb < rule.sink_blocks) keep = true;
+            if (qabs - kb < rule.window_blocks) keep = true;
+            if (kb < P && kb >= P - rule.local_blocks) keep = true;
+            float cv;
+            if (use_topk && kb < kend && cand_val(i, kb, cv)) {
+                if (take_all) {
+                    keep = true;
+                } else {
+                    const uint32_t key = order_key(cv);
+                    if (key > T || (key == T && kb <= eq_cut)) keep = true;
+                }
+            }
+        }
+        const uint64_t bal = __ballot(keep);
+        if (lane == 0) out[2 * c] = static_cast<uint32_t>(bal);
+        if (lane == 1 && 2 * c + 1 < s.words) out[2 * c + 1] = static_cast<uint32_t>(bal >> 32);
+    }
+}
+
 // ---------------------------------------------------------------------------------------
 // Block-Union + compaction, one (request, KV head) row per workgroup of 256 threads.
 struct UnionParams {
@@ -900,10 +1188,18 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
     p.rowmask = rowmask;
     const size_t lds = score_select_lds_bytes(s, compute);
     dim3 grid(s.B * s.Hq * s.Qb);
-    if (compute)
-        hipLaunchKernelGGL(row_select_kernel<true>, grid, dim3(kSelThreads), lds, stream, p);
+    // rows of up to 16 * 256 blocks (262144 tokens) in registers, longer ones through LDS
+    auto launch = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kSelThreads), lds, stream, p); };
+    if (s.cap <= 4 * kSelThreads)
+        compute ? launch(row_select_reg_kernel<true, 4>) : launch(row_select_reg_kernel<false, 4>);
+    else if (s.cap <= 8 * kSelThreads)
+        compute ? launch(row_select_reg_kernel<true, 8>) : launch(row_select_reg_kernel<false, 8>);
+    else if (s.cap <= 12 * kSelThreads)
+        compute ? launch(row_select_reg_kernel<true, 12>) : launch(row_select_reg_kernel<false, 12>);
+    else if (s.cap <= 16 * kSelThreads)
+        compute ? launch(row_select_reg_kernel<true, 16>) : launch(row_select_reg_kernel<false, 16>);
     else
-        hipLaunchKernelGGL(row_select_kernel<false>, grid, dim3(kSelThreads), lds, stream, p);
+        compute ? launch(row_select_kernel<true>) : launch(row_select_kernel<false>);
     return hipGetLastError();
 }
 

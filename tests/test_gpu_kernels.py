@@ -223,6 +223,28 @@ def test_score_select_bit_exact(gpu, rule_name, G):
     assert np.array_equal(unpack_rowmask(rowmask, cap), ref_keep)
 
 
+@pytest.mark.parametrize("past", [250, 1050, 2050, 3050, 4990])
+def test_score_select_row_lengths(gpu, past):
+    """Rows in every dispatch bucket of the selection kernel (the row held in 4, 8, 12 or 16
+    registers per thread, and the LDS-staged kernel beyond 4096 blocks): scores and masks bit
+    for bit, for the past-only and the all-columns top-k."""
+    _print_case(test="score_select_rows", past=past)
+    B, Hkv, G, Lq = 1, 1, 2, 128
+    Hq = Hkv * G
+    cap = past + Lq // 64 + 1
+    scale = 1.0 / math.sqrt(128)
+    g = torch.Generator().manual_seed(past)
+    qhat = torch.randn((B, Hq, Lq // 64, 128), generator=g)
+    khat = torch.randn((B * Hkv, cap, 128), generator=g)
+    ref_scores = oracle.block_scores(qhat.numpy(), khat.numpy().reshape(B, Hkv, cap, 128), [past], scale)
+    for rule in (oracle.Rule(topk=10, sink_blocks=1, local_blocks=2),
+                 oracle.Rule(topk=24, alpha=0.5, window_blocks=3, topk_all_columns=True)):
+        rowmask, scores = ops.score_select(qhat.to(gpu), khat.to(gpu), scale, _ops_rule(rule), [past], Hkv, cap,
+                                           with_scores=True)
+        assert float_bits_equal(f32(scores), ref_scores)
+        assert np.array_equal(unpack_rowmask(rowmask, cap), oracle.select_rows(ref_scores, [past], rule))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_select_scores_ties_and_nonfinite(gpu, dtype):
     _print_case(test="select_scores", dtype=dtype)
