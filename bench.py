@@ -140,8 +140,7 @@ def main() -> int:
     rule = ops.Rule(topk=topk, sink_blocks=1, local_blocks=2)
 
     def step():
-        ops.cache_fill(k_new, v_new, K, V, P, cap, kmean)
-        qhat = ops.pool_query(q, P, cap)
+        qhat = ops.cache_fill_pool_query(k_new, v_new, K, V, P, cap, kmean, q)
         rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, HKV, cap)
         table, counts, _, _ = ops.union_compact(rowmask, P, HKV, cap)
         ops.attn_fwd(q, K, V, table, counts, P, scale, cap, HKV, out=out, num_splits=splits, workspace=ws)
@@ -211,6 +210,7 @@ def main() -> int:
     qhat = ops.pool_query(q, P, cap)
     rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, HKV, cap)
     stage_fns = {
+        "cache_fill_pool_query": lambda: ops.cache_fill_pool_query(k_new, v_new, K, V, P, cap, kmean, q),
         "cache_fill": lambda: ops.cache_fill(k_new, v_new, K, V, P, cap, kmean),
         "pool_query": lambda: ops.pool_query(q, P, cap),
         "score_select": lambda: ops.score_select(qhat, kmean, scale, rule, P, HKV, cap),
@@ -261,6 +261,7 @@ def main() -> int:
     hbm_bytes = {
         "cache_fill": 2 * LQ * HKV * 128 * 2 * 2 + QB * HKV * 128 * 4,
         "pool_query": LQ * HQ * 128 * 2 + QB * HQ * 128 * 4,
+        "cache_fill_pool_query": (2 * LQ * HKV * 128 * 2 * 2 + QB * HKV * 128 * 4) + (LQ * HQ * 128 * 2 + QB * HQ * 128 * 4),
         "score_select": QB * HQ * 128 * 4 + (P[0] + QB) * HKV * 128 * 4 + HQ * QB * ((cap + 31) // 32) * 4,
         "union_compact": HQ * QB * ((cap + 31) // 32) * 4 + HKV * cap * 4 + HKV * 4,
     }
@@ -282,8 +283,8 @@ def main() -> int:
         "config": {
             "workload": f"config 2: {PAST}-token paged heads-first KV cache (page = block = 64) + {LQ}-token chunk, "
                         f"{HQ} Q / {HKV} KV heads, d 128, FlashPrefill pooled top-k selector at {args.keep:.0%} "
-                        "post-union keep + sink block 0 + 2 local blocks; one step = cache fill + scoring + "
-                        "selection + Block-Union + indexed attention",
+                        "post-union keep + sink block 0 + 2 local blocks; one step = cache fill with the pooled "
+                        "queries (one launch) + scoring + selection + Block-Union + indexed attention",
             "past_tokens": PAST, "chunk": LQ, "q_heads": HQ, "kv_heads": HKV, "block": 64,
             "topk_per_row": topk, "attn_splits": splits,
         },
@@ -388,8 +389,7 @@ def ragged_batch(dev, pasts=(16384, 49152, 98304, 131072), chunk=512, hq=28, hkv
                      device=dev)
 
     def step():
-        ops.cache_fill(k_new, v_new, K, V, P, cap, kmean)
-        qhat = ops.pool_query(q, P, cap)
+        qhat = ops.cache_fill_pool_query(k_new, v_new, K, V, P, cap, kmean, q)
         rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, hkv, cap)
         table, counts, _, _ = ops.union_compact(rowmask, P, hkv, cap)
         ops.attn_fwd(q, K, V, table, counts, P, scale, cap, hkv, out=out, num_splits=0, workspace=ws)

@@ -41,6 +41,7 @@ EXPORTED = (
     "ca_last_error",
     "ca_cache_fill",
     "ca_pool_query",
+    "ca_cache_fill_pool_query",
     "ca_gate_key_summaries",
     "ca_gate_query_summaries",
     "ca_score_select",
@@ -126,6 +127,8 @@ _SIGNATURES = {
     "ca_cache_fill": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(SeqLayout), _P(KvLayout), _P(KvLayout),
                                      _vp, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "ca_pool_query": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "ca_cache_fill_pool_query": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _P(SeqLayout), _P(KvLayout), _P(KvLayout),
+                                                _vp, _vp, _P(SeqLayout), _vp, _vp]),
     "ca_gate_key_summaries": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _i32, _vp, _i32, _vp, _vp, _i64, _vp,
                                              _vp]),
     "ca_gate_query_summaries": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _i32, _vp, _i32, _vp, _vp, _i64,

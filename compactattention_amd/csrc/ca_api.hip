@@ -322,6 +322,28 @@ int ca_gate_query_summaries(const ca_dims* dims, const ca_seq_layout* q, const i
     return ok();
 }
 
+int ca_cache_fill_pool_query(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_layout* v_new,
+                             const ca_kv_layout* k_cache, const ca_kv_layout* v_cache,
+                             const int32_t* past_blocks_host, float* kmean, const ca_seq_layout* q, float* qhat,
+                             void* stream) {
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    ca::SeqAddr kn{}, vn{}, qa{};
+    ca::KvAddr kc{}, vc{};
+    if ((rc = check_seq(k_new, "k_new", &kn)) != CA_OK) return rc;
+    if ((rc = check_seq(v_new, "v_new", &vn)) != CA_OK) return rc;
+    if ((rc = check_kv(k_cache, "k_cache", max_nkb, &kc)) != CA_OK) return rc;
+    if ((rc = check_kv(v_cache, "v_cache", max_nkb, &vc)) != CA_OK) return rc;
+    if ((rc = check_seq(q, "q", &qa)) != CA_OK) return rc;
+    if (kmean == nullptr || qhat == nullptr) return fail(CA_ERR_INVALID, "kmean and qhat are required");
+    if (!aligned16(kmean)) return fail(CA_ERR_INVALID, "kmean misaligned");
+    hipError_t e = ca::launch_chunk_summaries(s, kn, vn, kc, vc, pb, kmean, qa, qhat, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "cache_fill_pool_query launch");
+    return ok();
+}
+
 int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* past_blocks_host,
                   const float* gate_wq, const float* rope_cos, const float* rope_sin,
                   int64_t rope_rows, float* qhat, void* stream) {

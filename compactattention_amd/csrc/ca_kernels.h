@@ -42,6 +42,12 @@ hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr
                              float* kmean, const float* wk, const float* rope_cos,
                              const float* rope_sin, float* kgate, int pools, int gk, hipStream_t stream);
 
+// Cache append + mean-K (rows b*Hkv + h) and the query-block means (rows b*Hq + h) in one
+// launch: the FlashPrefill summaries of a chunk.
+hipError_t launch_chunk_summaries(const Shape& s, const SeqAddr& k_new, const SeqAddr& v_new, const KvAddr& k_cache,
+                                  const KvAddr& v_cache, const PastBlocks& pb, float* kmean, const SeqAddr& q,
+                                  float* qhat, hipStream_t stream);
+
 // pools: CA_POOL_* set; kv_aware: one output per KV head from its G heads' pooled vectors
 hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks& pb, const float* wq,
                              const float* rope_cos, const float* rope_sin, float* qhat, int pools,

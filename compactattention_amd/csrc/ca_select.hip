@@ -97,17 +97,13 @@ __device__ __forceinline__ int pool_count(int pools) {
 
 typedef uint32_t u32x4_v __attribute__((ext_vector_type(4)));
 
-// Cache fill: one (new block, request x KV head) per workgroup.
-__global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, SeqAddr vn,
-                                                         KvAddr kc, KvAddr vc, PastBlocks pb,
-                                                         float* kmean, const float* wk,
-                                                         const float* rope_cos,
-                                                         const float* rope_sin, float* kgate, int pools,
-                                                         int gk) {
-    __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
-    __shared__ float xs[3 * kD];
-    const int j = blockIdx.x;
-    const int row = blockIdx.y;
+// Cache fill of new block j of (request x KV head) `row` by one workgroup of 256 threads;
+// tile ([64][kTilePitch] bf16) and xs (3 * 128 floats) are its LDS.
+__device__ __forceinline__ void cache_fill_block(const Shape& s, const SeqAddr& kn, const SeqAddr& vn,
+                                                 const KvAddr& kc, const KvAddr& vc, const PastBlocks& pb,
+                                                 float* kmean, const float* wk, const float* rope_cos,
+                                                 const float* rope_sin, float* kgate, int pools, int gk, int j,
+                                                 int row, uint16_t* tile, float* xs) {
     const int b = row / s.Hkv;
     const int hk = row - b * s.Hkv;
     const int kb = pb.p[b] + j;
@@ -154,6 +150,19 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
     }
 }
 
+// Cache fill: one (new block, request x KV head) per workgroup.
+__global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, SeqAddr vn,
+                                                         KvAddr kc, KvAddr vc, PastBlocks pb,
+                                                         float* kmean, const float* wk,
+                                                         const float* rope_cos,
+                                                         const float* rope_sin, float* kgate, int pools,
+                                                         int gk) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
+    __shared__ float xs[3 * kD];
+    cache_fill_block(s, kn, vn, kc, vc, pb, kmean, wk, rope_cos, rope_sin, kgate, pools, gk, blockIdx.x, blockIdx.y,
+                     tile, xs);
+}
+
 // ---------------------------------------------------------------------------------------
 // Query-block summaries: the AttnGate pools (or the FlashPrefill mean) of one 64-token block,
 // optionally gate-projected and rotated.  One (block, request x head) per workgroup; with
@@ -162,14 +171,12 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
 // attn_gate.py:74-79,96-113).
 constexpr int kMaxGateIn = 16 * 3 * kD;  // G <= 16 heads x 3 pools x 128
 
-__global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, PastBlocks pb,
-                                                         const float* wq, const float* rope_cos,
-                                                         const float* rope_sin, float* qhat, int pools,
-                                                         int kv_aware) {
-    __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
-    __shared__ float xs[kMaxGateIn];
-    const int qb = blockIdx.x;
-    const int bh = blockIdx.y;
+// Summary of query block qb of (request x head) bh by one workgroup of 256 threads; xs holds
+// the pooled vectors (nsrc * pools * 128 floats).
+__device__ __forceinline__ void pool_query_block(const Shape& s, const SeqAddr& q, const PastBlocks& pb,
+                                                 const float* wq, const float* rope_cos, const float* rope_sin,
+                                                 float* qhat, int pools, int kv_aware, int qb, int bh,
+                                                 uint16_t* tile, float* xs) {
     const int heads = kv_aware ? s.Hkv : s.Hq;
     const int b = bh / heads;
     const int h = bh - b * heads;
@@ -200,6 +207,32 @@ __global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, Pas
     const int in = nsrc * C * kD;
     const float* w = wq != nullptr ? wq + (int64_t)h * in * kD : nullptr;
     if (t < 64) gate_project_rope(xs, in, w, rope_cos, rope_sin, (int64_t)pb.p[b] + qb, out, t);
+}
+
+__global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, PastBlocks pb,
+                                                         const float* wq, const float* rope_cos,
+                                                         const float* rope_sin, float* qhat, int pools,
+                                                         int kv_aware) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
+    __shared__ float xs[kMaxGateIn];
+    pool_query_block(s, q, pb, wq, rope_cos, rope_sin, qhat, pools, kv_aware, blockIdx.x, blockIdx.y, tile, xs);
+}
+
+// The chunk's FlashPrefill summaries in one launch: workgroup rows y < B*Hkv append the new
+// K/V blocks and write their mean-K (cache_fill_kernel without a gate), the others pool the
+// query blocks into their means (pool_query_kernel without a projection).
+__global__ __launch_bounds__(256) void chunk_summaries_kernel(Shape s, SeqAddr kn, SeqAddr vn, KvAddr kc,
+                                                              KvAddr vc, PastBlocks pb, float* kmean, SeqAddr q,
+                                                              float* qhat) {
+    __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
+    __shared__ float xs[3 * kD];
+    const int nkv = s.B * s.Hkv;
+    if ((int)blockIdx.y < nkv)
+        cache_fill_block(s, kn, vn, kc, vc, pb, kmean, nullptr, nullptr, nullptr, nullptr, CA_POOL_AVG, 1, blockIdx.x,
+                         blockIdx.y, tile, xs);
+    else
+        pool_query_block(s, q, pb, nullptr, nullptr, nullptr, qhat, CA_POOL_AVG, 0, blockIdx.x, blockIdx.y - nkv,
+                         tile, xs);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1144,6 +1177,15 @@ hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr
     dim3 grid(s.Qb, s.B * s.Hkv);
     hipLaunchKernelGGL(cache_fill_kernel, grid, dim3(256), 0, stream, s, k_new, v_new, k_cache,
                        v_cache, pb, kmean, wk, rope_cos, rope_sin, kgate, pools, gk);
+    return hipGetLastError();
+}
+
+hipError_t launch_chunk_summaries(const Shape& s, const SeqAddr& k_new, const SeqAddr& v_new, const KvAddr& k_cache,
+                                  const KvAddr& v_cache, const PastBlocks& pb, float* kmean, const SeqAddr& q,
+                                  float* qhat, hipStream_t stream) {
+    dim3 grid(s.Qb, s.B * (s.Hkv + s.Hq));
+    hipLaunchKernelGGL(chunk_summaries_kernel, grid, dim3(256), 0, stream, s, k_new, v_new, k_cache, v_cache, pb,
+                       kmean, q, qhat);
     return hipGetLastError();
 }
 

@@ -209,6 +209,27 @@ class PagedKVCache:
         self.length += L
         return past
 
+    def append_with_query_means(self, k_new: torch.Tensor, v_new: torch.Tensor,
+                                q: torch.Tensor) -> Tuple[int, torch.Tensor]:
+        """append(k_new, v_new) and the chunk's query-block means ([B, L, Hq, 128] bf16 ->
+        qhat [B, Hq, L/64, 128] fp32, the FlashPrefill pooled queries) in one kernel launch;
+        returns (past blocks before the append, qhat)."""
+        B, L, Hkv, _ = k_new.shape
+        if B != self.batch or Hkv != self.num_kv_heads:
+            raise ValueError("k_new does not match the cache's batch / KV heads")
+        if L % BLOCK:
+            raise ValueError("appended chunks must be multiples of 64 tokens")
+        if self.length % BLOCK:
+            raise ValueError("chunked prefill cannot follow decode steps that left a partial block")
+        if self.kmean is None:
+            raise ValueError("cache built without the mean-K summaries")
+        past = self.past_blocks
+        self._map(past, past + L // BLOCK)
+        K, V = self.layouts()
+        qhat = ops.cache_fill_pool_query(k_new, v_new, K, V, [past] * B, self.cap, self.kmean, q)
+        self.length += L
+        return past, qhat
+
     def append_tokens(self, k_new: torch.Tensor, v_new: torch.Tensor) -> int:
         """Decode append: [B, L, Hkv, 128] bf16 K/V (any L) at the current length, which need
         not be block-aligned; returns the length before the append.  Block summaries are

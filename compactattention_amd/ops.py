@@ -236,6 +236,33 @@ def pool_query(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, gate_wq
     return qhat
 
 
+def cache_fill_pool_query(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV, v_cache: KV,
+                          past_blocks: Sequence[int], kv_cap: int, kmean: torch.Tensor,
+                          q: torch.Tensor) -> torch.Tensor:
+    """cache_fill(k_new, v_new, k_cache, v_cache, past_blocks, kv_cap, kmean) and
+    pool_query(q, past_blocks, kv_cap) in one launch; returns qhat [B, Hq, Lq/64, 128] fp32."""
+    B, Lq, Hkv, _ = k_new.shape
+    Hq = q.shape[2]
+    if tuple(q.shape[:2]) != (B, Lq) or tuple(v_new.shape) != tuple(k_new.shape):
+        raise ValueError("q, k_new and v_new must cover the same [B, Lq] tokens")
+    if Hq % Hkv:
+        raise ValueError(f"num_q_heads={Hq} must be a multiple of num_kv_heads={Hkv}")
+    d = make_dims(B, Lq, Hq, Hkv, kv_cap)
+    kn, vn, ql = seq_layout(k_new, "k_new"), seq_layout(v_new, "v_new"), seq_layout(q, "q")
+    blocks = max(int(p) for p in past_blocks) + Lq // BLOCK
+    k_cache.check_blocks("k", B * Hkv, blocks)
+    v_cache.check_blocks("v", B * Hkv, blocks)
+    _need_cuda("kmean", kmean, torch.float32)
+    if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
+        raise ValueError("kmean must be contiguous [B*Hkv, kv_cap, 128] fp32")
+    qhat = torch.empty((B, Hq, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
+    check(_hip.lib().ca_cache_fill_pool_query(ctypes.byref(d), ctypes.byref(kn), ctypes.byref(vn),
+                                              ctypes.byref(k_cache.layout), ctypes.byref(v_cache.layout),
+                                              past_array(past_blocks), kmean.data_ptr(), ctypes.byref(ql),
+                                              qhat.data_ptr(), _stream()))
+    return qhat
+
+
 def _rope_args(rope_cos: Optional[torch.Tensor], rope_sin: Optional[torch.Tensor]) -> int:
     if (rope_cos is None) != (rope_sin is None):
         raise ValueError("rope_cos and rope_sin must both be given or both be None")

@@ -6,8 +6,9 @@ q/k/v projections, RoPE, cache update with the per-layer mean-K cache (:121-150)
 flashprefill_compactattn_prefill_full_kv for chunks with past context and dense attention
 for the first chunk, then o_proj.
 
-Execution per chunk: one ca_cache_fill appends the RoPE'd K/V pages and writes the fp32
-mean-K of the new blocks; ca_pool_query pools the RoPE'd queries; ca_score_select scores
+Execution per chunk: one ca_cache_fill_pool_query launch appends the RoPE'd K/V pages,
+writes the fp32 mean-K of the new blocks and pools the RoPE'd queries (a first or forced-dense
+chunk only appends, through ca_cache_fill); ca_score_select scores
 pooled Q.K blocks (softmax over causal key blocks, scale 1/sqrt(128)) and applies the
 FlashPrefill row rule (alpha * row max, sink, window, optional top-k budget);
 ca_union_compact leaves the last last_n_block query blocks out of the union; ca_attn_fwd
@@ -80,15 +81,17 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
         with event_span(self.attention_timer):
             query_states, key_states = rope_qk(q, k, cos, sin)
             cache = past_key_value.layer(self.layer_idx)
-            past = cache.append(key_states, v)  # pages + mean-K of the new blocks (v may be strided)
+            dense = cache.past_blocks == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
+            if dense:
+                past = cache.append(key_states, v)  # pages + mean-K of the new blocks (v may be strided)
+            else:  # the same append and the pooled queries in one launch
+                past, qhat = cache.append_with_query_means(key_states, v, query_states)
             P = [past] * B
-            dense = past == 0 or bool(self.config.seerattn_chunked_prefill_force_dense)
             if dense:
                 table, counts = ops.dense_table(P, L, self.num_heads, self.num_key_value_heads, cache.cap,
                                                 query_states.device)
             else:
                 rule = self._selection_rule()
-                qhat = ops.pool_query(query_states, P, cache.cap, num_kv_heads=self.num_key_value_heads)
                 rowmask, _ = ops.score_select(qhat, cache.kmean, 1.0 / math.sqrt(self.head_dim), rule, P,
                                               self.num_key_value_heads, cache.cap)
                 table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap,

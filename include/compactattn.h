@@ -140,6 +140,20 @@ int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* pa
                   int64_t rope_rows, float* qhat, void* stream);
 
 /*
+ * ca_cache_fill (append + mean-K, no gate) and ca_pool_query (query-block means, no
+ * projection) of one chunk in a single launch: dims->num_kv_heads sizes the cache side,
+ * num_q_heads the query side; k_new/v_new [B, q_len, Hkv, 128], q [B, q_len, Hq, 128].
+ * Results equal the two separate calls bit for bit.
+ * Replaces: the FlashPrefill model's per-chunk cache update + mean-K cache
+ * (modeling_llama_flashprefill_compactattn.py:121-150,205-246) and the query-side means of
+ * compute_block_score_chunked (flashprefill_native_forward.py:98-207).
+ */
+int ca_cache_fill_pool_query(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_layout* v_new,
+                             const ca_kv_layout* k_cache, const ca_kv_layout* v_cache,
+                             const int32_t* past_blocks_host, float* kmean, const ca_seq_layout* q, float* qhat,
+                             void* stream);
+
+/*
  * AttnGate block summaries for every gate type of the reference (compact_attn/prefill_sparse/
  * attn_gate.py:37-130,233-278: the Q{pools}_K{pools} classes, force_double, the
  * kv_group_aware_query form).  pools is a set of CA_POOL_* bits; the pooled vectors of a

@@ -90,6 +90,49 @@ def test_cache_fill_bit_exact(gpu, layout, gate):
             assert float_bits_equal(kg[b, :, past[b]:past[b] + qb], ref[b])
 
 
+@pytest.mark.parametrize("layout", ["heads_first", "paged"])
+def test_cache_fill_pool_query_equals_separate_calls(gpu, layout):
+    """The one-launch chunk summaries (cache append + mean-K + query-block means) against
+    ca_cache_fill and ca_pool_query called separately: cache, mean-K and qhat bit for bit,
+    with the means also against the oracle; a ragged batch at G = 3."""
+    _print_case(test="cache_fill_pool_query", layout=layout)
+    B, Lq, Hkv, G, past = 2, 192, 2, 3, [4, 11]
+    Hq = Hkv * G
+    qb = Lq // 64
+    cap = max(past) + qb + 1
+    g = torch.Generator().manual_seed(23)
+    k_new = torch.randn((B, Lq, Hkv, 128), generator=g).to(torch.bfloat16).to(gpu)
+    v_new = torch.randn((B, Lq, Hkv, 128), generator=g).to(torch.bfloat16).to(gpu)
+    q = torch.randn((B, Lq, Hq, 128), generator=g).to(torch.bfloat16).to(gpu)
+    out = []
+    for fused in (False, True):
+        if layout == "heads_first":
+            kc = torch.zeros((B, Hkv, cap * 64, 128), dtype=torch.bfloat16, device=gpu)
+            vc = torch.zeros_like(kc)
+            K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+        else:
+            rows = B * Hkv
+            pt = torch.randperm(rows * cap, generator=torch.Generator().manual_seed(5)).to(torch.int32)
+            pt = pt.view(rows, cap).contiguous().to(gpu)
+            kc = torch.zeros((rows * cap, 64, 128), dtype=torch.bfloat16, device=gpu)
+            vc = torch.zeros_like(kc)
+            K, V = ops.KV.paged(kc, pt), ops.KV.paged(vc, pt)
+        kmean = torch.full((B * Hkv, cap, 128), float("nan"), device=gpu)
+        if fused:
+            qhat = ops.cache_fill_pool_query(k_new, v_new, K, V, past, cap, kmean, q)
+        else:
+            ops.cache_fill(k_new, v_new, K, V, past, cap, kmean)
+            qhat = ops.pool_query(q, past, cap)
+        torch.cuda.synchronize()
+        out.append((kc.cpu(), vc.cpu(), f32(kmean), f32(qhat)))
+    for a, b in zip(out[0], out[1]):
+        if a.dtype == np.float32:
+            assert float_bits_equal(a, b)
+        else:
+            assert torch.equal(a, b)
+    assert float_bits_equal(out[1][3], oracle.block_mean(bits(q.cpu())))
+
+
 # ----------------------------------------------------------------------------- pooled Q
 @pytest.mark.parametrize("gate", [False, True])
 def test_pool_query_bit_exact(gpu, gate):
