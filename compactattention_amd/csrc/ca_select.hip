@@ -25,38 +25,40 @@ namespace {
 
 // ---------------------------------------------------------------------------------------
 // Gate projection (per head [in, 128], y[o] = sum_i x[i] W[i][o], sequential fma over
-// i = 0 .. in-1) and block RoPE y[i] = x[i] cos[i] + rotate_half(x)[i] sin[i].  64 threads
-// (t = 0..63); thread t owns the output pair (t, t + 64), which is exactly a rotate_half pair.
-// Without w the input (in = 128) is rotated as it is.
+// i = 0 .. in-1) and block RoPE y[i] = x[i] cos[i] + rotate_half(x)[i] sin[i] (t1 = x cos,
+// t2 = rot sin, y = t1 + t2).  128 threads per head: thread u owns output u; the weights of
+// 32 inputs are loaded before their fmas (in is a multiple of 128), and the rotate_half
+// partner of an output comes through ybuf ([128] floats of LDS).  Every thread of the
+// workgroup calls this (it holds barriers); `active` threads compute.  Without w the input
+// (in = 128) is rotated as it is.
 __device__ void gate_project_rope(const float* xs, int in, const float* w, const float* rope_cos,
-                                  const float* rope_sin, int64_t pos, float* out, int t) {
-    float a0 = 0.0f, a1 = 0.0f;
-    if (w == nullptr) {
-        a0 = xs[t];
-        a1 = xs[t + 64];
-    }
-    for (int i = 0; w != nullptr && i < in; ++i) {
-        const float x = xs[i];
-        a0 = __builtin_fmaf(x, w[i * kD + t], a0);
-        a1 = __builtin_fmaf(x, w[i * kD + t + 64], a1);
+                                  const float* rope_sin, int64_t pos, float* out, int u, bool active,
+                                  float* ybuf) {
+    float a = 0.0f;
+    if (active) {
+        if (w == nullptr) a = xs[u];
+        constexpr int kBatch = 32;
+        for (int i0 = 0; w != nullptr && i0 < in; i0 += kBatch) {
+            float wv[kBatch];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) wv[j] = w[(i0 + j) * kD + u];
+#pragma unroll
+            for (int j = 0; j < kBatch; ++j) a = __builtin_fmaf(xs[i0 + j], wv[j], a);
+        }
     }
     if (rope_cos == nullptr) {
-        out[t] = a0;
-        out[t + 64] = a1;
+        if (active) out[u] = a;
         return;
     }
-    const float* c = rope_cos + pos * kD;
-    const float* s = rope_sin + pos * kD;
-    {
-        const float t1 = a0 * c[t];
-        const float t2 = (-a1) * s[t];
-        out[t] = t1 + t2;
+    if (active) ybuf[u] = a;
+    __syncthreads();
+    if (active) {
+        const float rot = u < 64 ? -ybuf[u + 64] : ybuf[u - 64];
+        const float t1 = a * rope_cos[pos * kD + u];
+        const float t2 = rot * rope_sin[pos * kD + u];
+        out[u] = t1 + t2;
     }
-    {
-        const float t1 = a1 * c[t + 64];
-        const float t2 = a0 * s[t + 64];
-        out[t + 64] = t1 + t2;
-    }
+    __syncthreads();  // ybuf is free again
 }
 
 // ---------------------------------------------------------------------------------------
@@ -103,7 +105,7 @@ __device__ __forceinline__ void cache_fill_block(const Shape& s, const SeqAddr& 
                                                  const KvAddr& kc, const KvAddr& vc, const PastBlocks& pb,
                                                  float* kmean, const float* wk, const float* rope_cos,
                                                  const float* rope_sin, float* kgate, int pools, int gk, int j,
-                                                 int row, uint16_t* tile, float* xs) {
+                                                 int row, uint16_t* tile, float* xs, float* ybuf) {
     const int b = row / s.Hkv;
     const int hk = row - b * s.Hkv;
     const int kb = pb.p[b] + j;
@@ -141,12 +143,14 @@ __device__ __forceinline__ void cache_fill_block(const Shape& s, const SeqAddr& 
     if (wk == nullptr) return;
     __syncthreads();
     // gk gate heads per KV head: 1 (W_k per KV head) or G (the K block repeated to the Q heads
-    // hk*G + j and projected per Q head, attn_gate.py:30-33,84-86); four heads at a time
+    // hk*G + j and projected per Q head, attn_gate.py:30-33,84-86); two heads at a time
     const int in = kD * pool_count(pools);
-    for (int jh = t >> 6; jh < gk; jh += 4) {
-        const int64_t gh = (int64_t)row * gk + jh;  // gate-head row (b*Hkv + hk)*gk + jh
-        gate_project_rope(xs, in, wk + (int64_t)(hk * gk + jh) * in * kD, rope_cos, rope_sin, kb,
-                          kgate + (gh * s.cap + kb) * kD, t & 63);
+    for (int base = 0; base < gk; base += 2) {
+        const int jh = base + (t >> 7);
+        const bool active = jh < gk;
+        const int64_t gh = (int64_t)row * gk + (active ? jh : 0);  // gate-head row (b*Hkv + hk)*gk + jh
+        gate_project_rope(xs, in, wk + (int64_t)(hk * gk + (active ? jh : 0)) * in * kD, rope_cos, rope_sin, kb,
+                          kgate + (gh * s.cap + kb) * kD, t & 127, active, ybuf + 128 * (t >> 7));
     }
 }
 
@@ -159,8 +163,9 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
                                                          int gk) {
     __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
     __shared__ float xs[3 * kD];
+    __shared__ float ybuf[2 * kD];
     cache_fill_block(s, kn, vn, kc, vc, pb, kmean, wk, rope_cos, rope_sin, kgate, pools, gk, blockIdx.x, blockIdx.y,
-                     tile, xs);
+                     tile, xs, ybuf);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -169,14 +174,13 @@ __global__ __launch_bounds__(256) void cache_fill_kernel(Shape s, SeqAddr kn, Se
 // kv_aware one (block, request x KV head) per workgroup, whose G heads' pooled vectors are
 // concatenated (g-major) before a per-KV-head projection (kv_group_aware_query,
 // attn_gate.py:74-79,96-113).
-constexpr int kMaxGateIn = 16 * 3 * kD;  // G <= 16 heads x 3 pools x 128
 
 // Summary of query block qb of (request x head) bh by one workgroup of 256 threads; xs holds
 // the pooled vectors (nsrc * pools * 128 floats).
 __device__ __forceinline__ void pool_query_block(const Shape& s, const SeqAddr& q, const PastBlocks& pb,
                                                  const float* wq, const float* rope_cos, const float* rope_sin,
                                                  float* qhat, int pools, int kv_aware, int qb, int bh,
-                                                 uint16_t* tile, float* xs) {
+                                                 uint16_t* tile, float* xs, float* ybuf) {
     const int heads = kv_aware ? s.Hkv : s.Hq;
     const int b = bh / heads;
     const int h = bh - b * heads;
@@ -206,7 +210,7 @@ __device__ __forceinline__ void pool_query_block(const Shape& s, const SeqAddr& 
     __syncthreads();
     const int in = nsrc * C * kD;
     const float* w = wq != nullptr ? wq + (int64_t)h * in * kD : nullptr;
-    if (t < 64) gate_project_rope(xs, in, w, rope_cos, rope_sin, (int64_t)pb.p[b] + qb, out, t);
+    gate_project_rope(xs, in, w, rope_cos, rope_sin, (int64_t)pb.p[b] + qb, out, t & 127, t < 128, ybuf);
 }
 
 __global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, PastBlocks pb,
@@ -214,8 +218,10 @@ __global__ __launch_bounds__(256) void pool_query_kernel(Shape s, SeqAddr q, Pas
                                                          const float* rope_sin, float* qhat, int pools,
                                                          int kv_aware) {
     __shared__ __attribute__((aligned(16))) uint16_t tile[kBlock * kTilePitch];
-    __shared__ float xs[kMaxGateIn];
-    pool_query_block(s, q, pb, wq, rope_cos, rope_sin, qhat, pools, kv_aware, blockIdx.x, blockIdx.y, tile, xs);
+    __shared__ float ybuf[kD];
+    extern __shared__ float xs[];  // nsrc * pools * 128 pooled values (sized at launch)
+    pool_query_block(s, q, pb, wq, rope_cos, rope_sin, qhat, pools, kv_aware, blockIdx.x, blockIdx.y, tile, xs,
+                     ybuf);
 }
 
 // The chunk's FlashPrefill summaries in one launch: workgroup rows y < B*Hkv append the new
@@ -229,10 +235,10 @@ __global__ __launch_bounds__(256) void chunk_summaries_kernel(Shape s, SeqAddr k
     const int nkv = s.B * s.Hkv;
     if ((int)blockIdx.y < nkv)
         cache_fill_block(s, kn, vn, kc, vc, pb, kmean, nullptr, nullptr, nullptr, nullptr, CA_POOL_AVG, 1, blockIdx.x,
-                         blockIdx.y, tile, xs);
+                         blockIdx.y, tile, xs, nullptr);
     else
         pool_query_block(s, q, pb, nullptr, nullptr, nullptr, qhat, CA_POOL_AVG, 0, blockIdx.x, blockIdx.y - nkv,
-                         tile, xs);
+                         tile, xs, nullptr);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -1193,7 +1199,9 @@ hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks&
                              const float* rope_cos, const float* rope_sin, float* qhat, int pools,
                              bool kv_aware, hipStream_t stream) {
     dim3 grid(s.Qb, s.B * (kv_aware ? s.Hkv : s.Hq));
-    hipLaunchKernelGGL(pool_query_kernel, grid, dim3(256), 0, stream, s, q, pb, wq, rope_cos,
+    // the pooled vectors of one output: G heads (kv-aware) or one, times the pools
+    const size_t xs_bytes = sizeof(float) * kD * (kv_aware ? s.G : 1) * __builtin_popcount(pools & 7);
+    hipLaunchKernelGGL(pool_query_kernel, grid, dim3(256), xs_bytes, stream, s, q, pb, wq, rope_cos,
                        rope_sin, qhat, pools, kv_aware ? 1 : 0);
     return hipGetLastError();
 }
