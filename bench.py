@@ -53,6 +53,7 @@ def parse():
     ap.add_argument("--no-ragged", action="store_true", help="skip the config-4 ragged batch")
     ap.add_argument("--no-decode", action="store_true", help="skip the dense decode lines")
     ap.add_argument("--no-module", action="store_true", help="skip the module-level attention time")
+    ap.add_argument("--no-shard", action="store_true", help="skip the 2-way KV-head sharding share")
     ap.add_argument("--model-tokens", type=int, default=131072)
     ap.add_argument("--model-chunk", type=int, default=2048)
     ap.add_argument("--model-layers", type=int, default=32)
@@ -324,6 +325,11 @@ def main() -> int:
         result["decode"] = decode_lines(dev)
     del ch, kc, vc, K, V, kmean, ws, dws
     torch.cuda.empty_cache()
+    if not args.no_shard:
+        progress("one GPU's share of 2-way KV-head sharding")
+        result["tp2_share"] = shard_share(dev, PAST, LQ, HQ // 2, HKV // 2, args.keep)
+    torch.cuda.empty_cache()
+    torch.cuda.empty_cache()
     if not args.no_module:
         progress("module-level attention (the reference's self_attn.forward definition)")
         result["module_attention"] = module_attention(dev, PAST, LQ, args.keep)
@@ -333,6 +339,98 @@ def main() -> int:
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+def shard_share(dev, past: int, chunk: int, hq: int, hkv: int, keep: float, steps: int = 20):
+    """One GPU's share of the config-2 step under 2-way KV-head sharding (the reference's TP:
+    q/k/v column-parallel, each rank owning hkv KV groups and their hq query heads): the same
+    kernels on that shape, one rank's paged cache, summaries, selection and attention.  The
+    ranks exchange nothing on this path (the row-parallel o_proj all-reduce follows it);
+    nothing here uses a second GPU."""
+    import torch
+
+    from compactattention_amd import ops
+    from compactattention_amd.synthetic import make_chunk_device
+
+    qb = chunk // 64
+    scale = 1.0 / math.sqrt(128)
+    ch = make_chunk_device(past, chunk, hq, hkv, dev)
+    cap, P, q = ch.kv_cap, ch.past_blocks, ch.q
+    kc, vc = torch.zeros_like(ch.k), torch.zeros_like(ch.v)
+    K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+    kmean = torch.zeros((hkv, cap, 128), dtype=torch.float32, device=dev)
+    for t0 in range(0, past, 16384):
+        t1 = min(past, t0 + 16384)
+        ops.cache_fill(ch.k[:, :, t0:t1].transpose(1, 2).contiguous(), ch.v[:, :, t0:t1].transpose(1, 2).contiguous(),
+                       K, V, [t0 // 64], cap, kmean)
+    k_new = ch.k[:, :, past:past + chunk].transpose(1, 2).contiguous()
+    v_new = ch.v[:, :, past:past + chunk].transpose(1, 2).contiguous()
+    del ch
+    out = torch.empty_like(q)
+    splits = ops.attn_pick_splits(P, chunk, hq, hkv, cap)
+    ws = torch.empty((max(ops.attn_workspace_bytes(P, chunk, hq, hkv, cap, splits), 16),), dtype=torch.uint8,
+                     device=dev)
+
+    def select(topk):
+        rule = ops.Rule(topk=topk, sink_blocks=1, local_blocks=2)
+        qhat = ops.pool_query(q, P, cap)
+        rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, hkv, cap)
+        return ops.union_compact(rowmask, P, hkv, cap)[:2]
+
+    def keep_of(counts):
+        return float((counts.float() - qb).mean().item()) / P[0]
+
+    lo, hi, best = 1, P[0], None
+    while lo <= hi:
+        mid = (lo + hi) // 2
+        r = keep_of(select(mid)[1])
+        if best is None or abs(r - keep) < abs(best[1] - keep):
+            best = (mid, r)
+        lo, hi = (mid + 1, hi) if r < keep else (lo, mid - 1)
+    rule = ops.Rule(topk=best[0], sink_blocks=1, local_blocks=2)
+
+    def step():
+        qhat = ops.cache_fill_pool_query(k_new, v_new, K, V, P, cap, kmean, q)
+        rowmask, _ = ops.score_select(qhat, kmean, scale, rule, P, hkv, cap)
+        table, counts, _, _ = ops.union_compact(rowmask, P, hkv, cap)
+        ops.attn_fwd(q, K, V, table, counts, P, scale, cap, hkv, out=out, num_splits=splits, workspace=ws)
+        return table, counts
+
+    end = time.perf_counter() + 0.5  # clocks to steady state, as for the headline step
+    while time.perf_counter() < end:
+        step()
+        torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        table, counts = step()
+    torch.cuda.synchronize()
+    path_us = (time.perf_counter() - t0) / steps * 1e6
+
+    def ev_time(fn, n=10):
+        fn()
+        a, b_ = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b_.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b_) / n * 1e3
+
+    attn_us = ev_time(lambda: ops.attn_fwd(q, K, V, table, counts, P, scale, cap, hkv, out=out, num_splits=splits,
+                                           workspace=ws))
+    G = hq // hkv
+    fl = sum(4.0 * 128 * G * (chunk * (int(c) - qb) * 64 + chunk * (chunk + 1) / 2) for c in counts.cpu().tolist())
+    return {
+        "workload": f"config 2 per rank of 2-way KV-head sharding: {past}-token paged cache, {chunk}-token chunk, "
+                    f"{hq} Q / {hkv} KV heads, FlashPrefill top-k at ~{keep:.0%} keep; one GPU",
+        "path_us": round(path_us, 1),
+        "attn_us": round(attn_us, 1),
+        "attn_tflops": round(fl / (attn_us * 1e-6) / 1e12, 1),
+        "attn_frac": round(fl / (attn_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "keep_ratio": round(keep_of(counts), 4),
+        "topk_per_row": best[0],
+        "attn_splits": splits,
+    }
 
 
 def ragged_batch(dev, pasts=(16384, 49152, 98304, 131072), chunk=512, hq=28, hkv=4, keep=0.20):

@@ -76,9 +76,11 @@ struct AttnParams {
     int32_t nkb[CA_MAX_BATCH];       // valid logical blocks of each request
     int32_t sp[CA_MAX_BATCH];        // splits of each request's block lists
     int32_t ioff[CA_MAX_BATCH + 1];  // first work item of each request (linear placement)
-    int use_rows;                    // rows placed per XCD (xrow / xoff)
+    int use_rows;                    // units placed per XCD (xoff / xrow / xlo / xcnt)
     int32_t xoff[9];
     uint16_t xrow[kPlanRows];
+    uint8_t xlo[kPlanRows];
+    uint8_t xcnt[kPlanRows];
 };
 
 __device__ __forceinline__ int swap23(int m) {
@@ -131,19 +133,20 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int x = L & 7;
     int k = L >> 3;
     const Shape& s = p.s;
-    int row, b, local;
+    int row, b, split, tile;
     if (p.use_rows) {
         int i = p.xoff[x];
         const int iend = p.xoff[x + 1];
         for (; i < iend; ++i) {
-            const int items = p.ntiles * p.sp[p.xrow[i] / s.Hkv];
+            const int items = p.ntiles * p.xcnt[i];
             if (k < items) break;
             k -= items;
         }
         if (i >= iend) return;
         row = p.xrow[i];
         b = row / s.Hkv;
-        local = k;
+        split = p.xlo[i] + k % p.xcnt[i];
+        tile = k / p.xcnt[i];
     } else {
         const int W = x * p.per_xcd + k;
         if (W >= p.total_items) return;
@@ -151,12 +154,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         while (b + 1 < s.B && p.ioff[b + 1] <= W) ++b;
         const int per_row = p.ntiles * p.sp[b];
         row = b * s.Hkv + (W - p.ioff[b]) / per_row;
-        local = (W - p.ioff[b]) % per_row;
+        const int local = (W - p.ioff[b]) % per_row;
+        split = local % p.sp[b];
+        tile = local / p.sp[b];
     }
     const int hk = row - b * s.Hkv;
     const int nsplit = p.sp[b];
-    const int split = local % nsplit;
-    const int tile = local / nsplit;
     const int G = s.G;
     const int qpos0 = p.qpos0[b];  // query row t sits at absolute position qpos0 + t
     const int nkb = p.nkb[b];      // valid logical block ids are [0, nkb)
@@ -532,19 +535,19 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams 
     const int x = L & 7;
     int k = L >> 3;
     const Shape& s = p.s;
-    int row, b, local;
+    int row, b, split;
     if (p.use_rows) {
         int i = p.xoff[x];
         const int iend = p.xoff[x + 1];
         for (; i < iend; ++i) {
-            const int items = p.sp[p.xrow[i] / s.Hkv];
+            const int items = p.xcnt[i];
             if (k < items) break;
             k -= items;
         }
         if (i >= iend) return;
         row = p.xrow[i];
         b = row / s.Hkv;
-        local = k;
+        split = p.xlo[i] + k;
     } else {
         const int W = x * p.per_xcd + k;
         if (W >= p.total_items) return;
@@ -552,11 +555,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams 
         while (b + 1 < s.B && p.ioff[b + 1] <= W) ++b;
         const int per_row = p.sp[b];
         row = b * s.Hkv + (W - p.ioff[b]) / per_row;
-        local = (W - p.ioff[b]) % per_row;
+        split = (W - p.ioff[b]) % per_row;
     }
     const int hk = row - b * s.Hkv;
     const int nsplit = p.sp[b];
-    const int split = local;
     const int G = s.G;
     const int R = p.rows_total;
     const int qpos0 = p.qpos0[b];
@@ -856,37 +858,58 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
         plan->per_xcd = (plan->off[s.B] + 7) / 8;
         return;
     }
-    // rows longest first (stable), each to the XCD with the least work so far
+    // placement units, longest first (stable), each to the XCD with the least work so far:
+    // whole rows, or with fewer rows than XCDs up to 8 / rows groups of each row's splits
+    int unit_row[kPlanRows], unit_lo[kPlanRows], unit_cnt[kPlanRows];
+    double unit_work[kPlanRows];  // blocks x row tiles the unit's items stream
+    int units = 0;
+    for (int r = 0; r < rows; ++r) {
+        const int sp = plan->s[r / s.Hkv];
+        const int m = rows < 8 ? max(1, min(sp, 8 / rows)) : 1;
+        for (int g = 0; g < m; ++g) {
+            const int lo = g * sp / m;
+            const int hi = (g + 1) * sp / m;
+            unit_row[units] = r;
+            unit_lo[units] = lo;
+            unit_cnt[units] = hi - lo;
+            unit_work[units] = (double)nkb[r / s.Hkv] * ntiles * (hi - lo) / sp;
+            ++units;
+        }
+    }
     int order[kPlanRows];
-    for (int r = 0; r < rows; ++r) order[r] = r;
-    auto work = [&](int r) { return nkb[r / s.Hkv]; };
-    for (int i = 1; i < rows; ++i) {
-        const int r = order[i];
+    for (int u = 0; u < units; ++u) order[u] = u;
+    for (int i = 1; i < units; ++i) {
+        const int u = order[i];
         int j = i;
-        while (j > 0 && work(order[j - 1]) < work(r)) {
+        while (j > 0 && unit_work[order[j - 1]] < unit_work[u]) {
             order[j] = order[j - 1];
             --j;
         }
-        order[j] = r;
+        order[j] = u;
     }
-    int64_t load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int items[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-    int nrow[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int nunit[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint16_t lists[8][kPlanRows];
-    for (int i = 0; i < rows; ++i) {
-        const int r = order[i];
+    for (int i = 0; i < units; ++i) {
+        const int u = order[i];
         int x = 0;
         for (int c = 1; c < 8; ++c)
             if (load[c] < load[x] || (load[c] == load[x] && items[c] < items[x])) x = c;
-        lists[x][nrow[x]++] = static_cast<uint16_t>(r);
-        load[x] += (int64_t)work(r) * ntiles;
-        items[x] += ntiles * plan->s[r / s.Hkv];
+        lists[x][nunit[x]++] = static_cast<uint16_t>(u);
+        load[x] += unit_work[u];
+        items[x] += ntiles * unit_cnt[u];
     }
     plan->xoff[0] = 0;
     plan->per_xcd = 0;
     for (int x = 0; x < 8; ++x) {
-        for (int i = 0; i < nrow[x]; ++i) plan->xrow[plan->xoff[x] + i] = lists[x][i];
-        plan->xoff[x + 1] = plan->xoff[x] + nrow[x];
+        for (int i = 0; i < nunit[x]; ++i) {
+            const int u = lists[x][i];
+            plan->xrow[plan->xoff[x] + i] = static_cast<uint16_t>(unit_row[u]);
+            plan->xlo[plan->xoff[x] + i] = static_cast<uint8_t>(unit_lo[u]);
+            plan->xcnt[plan->xoff[x] + i] = static_cast<uint8_t>(unit_cnt[u]);
+        }
+        plan->xoff[x + 1] = plan->xoff[x] + nunit[x];
         plan->per_xcd = max(plan->per_xcd, items[x]);
     }
 }
@@ -944,7 +967,12 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     p.per_xcd = plan.per_xcd;
     p.use_rows = plan.use_rows;
     for (int x = 0; x < 9; ++x) p.xoff[x] = plan.use_rows ? plan.xoff[x] : 0;
-    for (int i = 0; i < kPlanRows; ++i) p.xrow[i] = plan.use_rows && i < plan.xoff[8] ? plan.xrow[i] : 0;
+    for (int i = 0; i < kPlanRows; ++i) {
+        const bool used = plan.use_rows && i < plan.xoff[8];
+        p.xrow[i] = used ? plan.xrow[i] : 0;
+        p.xlo[i] = used ? plan.xlo[i] : 0;
+        p.xcnt[i] = used ? plan.xcnt[i] : 1;
+    }
     const int64_t rows_all = (int64_t)a.s.B * a.s.Hkv * p.rows_total;
     p.ws_o = plan.max > 1 ? static_cast<float*>(a.workspace) : nullptr;
     p.ws_lse = plan.max > 1 ? p.ws_o + (int64_t)plan.max * rows_all * 128 : nullptr;

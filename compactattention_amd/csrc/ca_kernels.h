@@ -93,7 +93,10 @@ constexpr int kMaxDecodeSplits = 64;
 // Split-KV plan.  Request b's block lists are cut into s[b] pieces (max = the largest,
 // which sizes the workspace).  Work placement: with at most kPlanRows KV rows, whole rows
 // go to XCDs (longest first, each to the least-loaded XCD), so a row's items share one L2
-// and the XCDs carry equal work: xrow[xoff[x] .. xoff[x+1]) lists XCD x's rows in order.
+// and the XCDs carry equal work: entries xoff[x] .. xoff[x+1] list XCD x's units in order,
+// each a row (xrow) and a range of its splits (xlo, xcnt).  With fewer rows than XCDs a
+// row's splits are cut into groups on different XCDs, whose items stream disjoint parts of
+// the row's block list.
 // Otherwise items are numbered request by request (off[b]) and dealt to XCDs in
 // contiguous ranges.
 constexpr int kPlanRows = 512;
@@ -103,7 +106,9 @@ struct SplitPlan {
     int max;
     int use_rows;
     int per_xcd;  // work items per XCD (grid = 8 * per_xcd)
-    uint16_t xrow[kPlanRows];
+    uint16_t xrow[kPlanRows];  // placement units: a row and a range of its splits
+    uint8_t xlo[kPlanRows];    // first split of the unit
+    uint8_t xcnt[kPlanRows];   // splits in the unit
     int32_t xoff[9];
 };
 

@@ -327,3 +327,30 @@ def test_fullsize_config4_ragged(gpu):
     kept = [float(((counts.cpu().view(B, hkv)[b] - qb).float() / P[b]).mean()) for b in range(B)]
     assert all(0.05 < r < 0.5 for r in kept), kept
     _check_attention(q, k, v, P, table, counts, cap, hkv, oracle_rows=((0, 2), (lq - 2, lq)))
+
+
+# ------------------------------------------------------- one rank's share of 2-way sharding
+@pytest.mark.parametrize("hkv", [4, 2])
+def test_sharded_share_fewer_rows_than_xcds(gpu, hkv):
+    """One GPU's share of config 2 under KV-head sharding (2 and 4 ways: 4 / 16 and 2 / 8 KV /
+    Q heads of a 131072-token cache): fewer KV rows than the 8 XCDs, so the plan places
+    groups of each row's splits on different XCDs.  Tables bit-exact against the oracle,
+    every attention row against the fp32 torch reference, and the result equal to the one
+    split-count plan within the same tolerance."""
+    hq = hkv * HQ // HKV
+    print(f"case: sharded share (131072 past tokens, chunk 1024, {hq}/{hkv} heads)", flush=True)
+    ch = make_chunk_device(PAST, LQ, hq, hkv, gpu, seed=91)
+    cap, P = ch.kv_cap, ch.past_blocks
+    assert ops.attn_pick_splits(P, LQ, hq, hkv, cap) >= 8 // hkv
+    kc, vc = torch.zeros_like(ch.k), torch.zeros_like(ch.v)
+    K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+    kmean = torch.zeros((hkv, cap, 128), dtype=torch.float32, device=gpu)
+    _fill(ch, K, V, kmean, PAST, LQ)
+    qhat = ops.pool_query(ch.q, P, cap)
+    rowmask, table, counts = _select(qhat, kmean, P, hkv, cap, TOPK)
+    _, _, sc = _oracle_scores(ch)
+    _check_tables(rowmask, table, counts, sc, P, hkv, cap, TOPK)
+    out = _check_attention(ch.q, kc, vc, P, table, counts, cap, hkv, oracle_rows=((LQ - 2, LQ),))
+    one = ops.attn_fwd(ch.q, K, V, table, counts, P, SCALE, cap, hkv, num_splits=1)
+    err = (out.float() - one.float()).abs()
+    assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
