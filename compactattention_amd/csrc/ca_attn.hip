@@ -859,13 +859,15 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
         return;
     }
     // placement units, longest first (stable), each to the XCD with the least work so far:
-    // whole rows, or with fewer rows than XCDs up to 8 / rows groups of each row's splits
+    // whole rows when the rows divide evenly over the 8 XCDs, otherwise single splits of a
+    // row (its split ranges are disjoint parts of the block list, so placing them apart
+    // duplicates only the row's query reads)
     int unit_row[kPlanRows], unit_lo[kPlanRows], unit_cnt[kPlanRows];
     double unit_work[kPlanRows];  // blocks x row tiles the unit's items stream
     int units = 0;
     for (int r = 0; r < rows; ++r) {
         const int sp = plan->s[r / s.Hkv];
-        const int m = rows < 8 ? max(1, min(sp, 8 / rows)) : 1;
+        const int m = rows % 8 == 0 ? 1 : sp;
         for (int g = 0; g < m; ++g) {
             const int lo = g * sp / m;
             const int hi = (g + 1) * sp / m;

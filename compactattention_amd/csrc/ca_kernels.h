@@ -94,9 +94,9 @@ constexpr int kMaxDecodeSplits = 64;
 // which sizes the workspace).  Work placement: with at most kPlanRows KV rows, whole rows
 // go to XCDs (longest first, each to the least-loaded XCD), so a row's items share one L2
 // and the XCDs carry equal work: entries xoff[x] .. xoff[x+1] list XCD x's units in order,
-// each a row (xrow) and a range of its splits (xlo, xcnt).  With fewer rows than XCDs a
-// row's splits are cut into groups on different XCDs, whose items stream disjoint parts of
-// the row's block list.
+// each a row (xrow) and a range of its splits (xlo, xcnt).  When the rows do not divide
+// evenly over the XCDs, each split of a row is a unit of its own, so the XCDs' loads even
+// out; its items stream a disjoint part of the row's block list.
 // Otherwise items are numbered request by request (off[b]) and dealt to XCDs in
 // contiguous ranges.
 constexpr int kPlanRows = 512;

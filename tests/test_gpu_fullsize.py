@@ -330,13 +330,13 @@ def test_fullsize_config4_ragged(gpu):
 
 
 # ------------------------------------------------------- one rank's share of 2-way sharding
-@pytest.mark.parametrize("hkv", [4, 2])
+@pytest.mark.parametrize("hkv", [4, 2, 6])
 def test_sharded_share_fewer_rows_than_xcds(gpu, hkv):
     """One GPU's share of config 2 under KV-head sharding (2 and 4 ways: 4 / 16 and 2 / 8 KV /
-    Q heads of a 131072-token cache): fewer KV rows than the 8 XCDs, so the plan places
-    groups of each row's splits on different XCDs.  Tables bit-exact against the oracle,
-    every attention row against the fp32 torch reference, and the result equal to the one
-    split-count plan within the same tolerance."""
+    Q heads of a 131072-token cache) and a 6 / 24-head shape: KV rows that do not divide over
+    the 8 XCDs, so the plan places single splits of each row on different XCDs.  Tables
+    bit-exact against the oracle, every attention row against the fp32 torch reference, and
+    the result equal to the unsplit plan within the same tolerance."""
     hq = hkv * HQ // HKV
     print(f"case: sharded share (131072 past tokens, chunk 1024, {hq}/{hkv} heads)", flush=True)
     ch = make_chunk_device(PAST, LQ, hq, hkv, gpu, seed=91)
