@@ -858,16 +858,27 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
         plan->per_xcd = (plan->off[s.B] + 7) / 8;
         return;
     }
-    // placement units, longest first (stable), each to the XCD with the least work so far:
-    // whole rows when the rows divide evenly over the 8 XCDs, otherwise single splits of a
-    // row (its split ranges are disjoint parts of the block list, so placing them apart
-    // duplicates only the row's query reads)
+    // Placement units on the 8 XCDs.  A unit is a KV row and a range of its splits; the row
+    // tiles of a unit stream the same blocks, so they share the XCD's L2, and different
+    // split ranges of a row are disjoint parts of its block list (placing them apart
+    // duplicates only the row's query reads).
+    //  - Requests of one length over a multiple of 8 rows: whole rows, longest first, each
+    //    to the least-loaded XCD (config 2 and 3: one or more rows per XCD).
+    //  - Otherwise (rows that do not divide over the XCDs, or ragged lengths): single
+    //    splits, dealt round-robin over the XCDs request by request, so every XCD gets an
+    //    equal share of every request's work whatever the rows' selected counts turn out to
+    //    be (the host only knows their past lengths); each XCD runs its units longest first.
+    bool same_len = true;
+    for (int b = 1; b < s.B; ++b) same_len = same_len && nkb[b] == nkb[0];
+    int nunits = 0;
+    for (int r = 0; r < rows; ++r) nunits += plan->s[r / s.Hkv];
+    const bool split_units = (rows % 8 != 0 || !same_len) && nunits <= kPlanRows;
     int unit_row[kPlanRows], unit_lo[kPlanRows], unit_cnt[kPlanRows];
     double unit_work[kPlanRows];  // blocks x row tiles the unit's items stream
     int units = 0;
     for (int r = 0; r < rows; ++r) {
         const int sp = plan->s[r / s.Hkv];
-        const int m = rows % 8 == 0 ? 1 : sp;
+        const int m = split_units ? sp : 1;
         for (int g = 0; g < m; ++g) {
             const int lo = g * sp / m;
             const int hi = (g + 1) * sp / m;
@@ -878,28 +889,45 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
             ++units;
         }
     }
-    int order[kPlanRows];
-    for (int u = 0; u < units; ++u) order[u] = u;
-    for (int i = 1; i < units; ++i) {
-        const int u = order[i];
-        int j = i;
-        while (j > 0 && unit_work[order[j - 1]] < unit_work[u]) {
-            order[j] = order[j - 1];
-            --j;
-        }
-        order[j] = u;
-    }
+    int xcd_of[kPlanRows];
     double load[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int items[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (split_units) {
+        for (int u = 0; u < units; ++u) xcd_of[u] = u % 8;  // request-major unit order
+    } else {
+        int order[kPlanRows];
+        for (int u = 0; u < units; ++u) order[u] = u;
+        for (int i = 1; i < units; ++i) {  // longest first, stable
+            const int u = order[i];
+            int j = i;
+            while (j > 0 && unit_work[order[j - 1]] < unit_work[u]) {
+                order[j] = order[j - 1];
+                --j;
+            }
+            order[j] = u;
+        }
+        for (int i = 0; i < units; ++i) {
+            const int u = order[i];
+            int x = 0;
+            for (int c = 1; c < 8; ++c)
+                if (load[c] < load[x] || (load[c] == load[x] && items[c] < items[x])) x = c;
+            xcd_of[u] = x;
+            load[x] += unit_work[u];
+            items[x] += ntiles * unit_cnt[u];
+        }
+    }
+    // each XCD's units, longest first (stable)
     int nunit[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     uint16_t lists[8][kPlanRows];
-    for (int i = 0; i < units; ++i) {
-        const int u = order[i];
-        int x = 0;
-        for (int c = 1; c < 8; ++c)
-            if (load[c] < load[x] || (load[c] == load[x] && items[c] < items[x])) x = c;
-        lists[x][nunit[x]++] = static_cast<uint16_t>(u);
-        load[x] += unit_work[u];
+    for (int x = 0; x < 8; ++x) items[x] = 0;
+    for (int u = 0; u < units; ++u) {
+        const int x = xcd_of[u];
+        int j = nunit[x]++;
+        while (j > 0 && unit_work[lists[x][j - 1]] < unit_work[u]) {
+            lists[x][j] = lists[x][j - 1];
+            --j;
+        }
+        lists[x][j] = static_cast<uint16_t>(u);
         items[x] += ntiles * unit_cnt[u];
     }
     plan->xoff[0] = 0;
