@@ -279,8 +279,10 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
  * count for the launch (ca_attn_pick_splits) with at least ~16 blocks per split: about 256
  * work items (row tiles x splits, one per CU) when all requests have one length, 1 when
  * their row tiles alone fill three quarters of the 256 CUs, and about 512 for ragged
- * batches.  Whole KV rows are placed on the XCDs longest-first either way.  More than one split needs a workspace of
- * ca_attn_workspace_size(dims, past, num_splits) bytes.
+ * batches.  The work is placed on the 8 XCDs in units: whole KV rows (longest first) when
+ * the requests have one length and the rows divide over the XCDs, otherwise single splits
+ * of each row dealt round-robin request by request.  More than one split needs a workspace
+ * of ca_attn_workspace_size(dims, past, num_splits) bytes.
  * Replaces: flash_attn_with_kvcache / FlashInfer paged prefill as driven by
  * flash_attn_indexed_prefill_from_paged_kv (compact_attn/kernels/varlen/
  * indexed_dense_prefill_varlen.py:1473-1613) and flashinfer_prefill_zero_copy
