@@ -57,6 +57,8 @@ def parse():
     ap.add_argument("--model-tokens", type=int, default=131072)
     ap.add_argument("--model-chunk", type=int, default=2048)
     ap.add_argument("--model-layers", type=int, default=32)
+    ap.add_argument("--model-only", action="store_true",
+                    help="only the config-3 Seer model prefill (one JSON line; for kernel traces of the model)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three plain 256 MiB device copies (the HBM counter calibration under rocprofv3)")
     return ap.parse_args()
@@ -84,6 +86,11 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.model_only:
+        seer = model_prefill(args.model_tokens, args.model_chunk, args.model_layers, dev, seer_only=True)
+        print(json.dumps({"metric": "config-3 Seer compactattn model prefill tok/s", "value": seer["tok_per_s"],
+                          "unit": "tok/s", "higher_is_better": True, "n_gpus": 1, "model_prefill": seer}), flush=True)
+        return 0
     PAST, LQ, HQ, HKV = args.past, args.chunk, args.q_heads, args.kv_heads
     G = HQ // HKV
     QB = LQ // 64
@@ -656,7 +663,7 @@ def _prefill_run(model, ids, chunk, cache):
     return secs, flops, attn_s, wall, sum(keeps) / max(len(keeps), 1)
 
 
-def model_prefill(tokens, chunk, layers, dev):
+def model_prefill(tokens, chunk, layers, dev, seer_only: bool = False):
     """whole-model chunked prefill of a Llama-3.1-8B-shaped decoder with
     random N(0, 0.02) bf16 weights, AttnGate (Seer selector, softmax threshold 5e-3 + sink
     block + 2 local blocks) at every layer, first chunk dense; next to the same model with
@@ -694,6 +701,8 @@ def model_prefill(tokens, chunk, layers, dev):
     progress("model prefill: Seer AttnGate")
     seer = line(*_prefill_run(model, ids, chunk, cache))
     progress(f"model prefill: Seer {seer['seconds']:.2f} s")
+    if seer_only:
+        return seer
     cfg.seerattn_chunked_prefill_force_dense = True
     dense = line(*_prefill_run(model, ids, chunk, cache))
     progress(f"model prefill: dense {dense['seconds']:.2f} s")
