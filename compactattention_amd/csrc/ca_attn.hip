@@ -72,6 +72,10 @@ struct AttnParams {
     int per_xcd;      // ceil(total_items / 8)
     float* ws_o;      // [max splits][B*Hkv][rows_total][128]
     float* ws_lse;    // [max splits][B*Hkv][rows_total]  (log2 domain)
+    // Ragged prefill whose row tiles fill 3/4 of the CUs: the kernel runs unsplit when every
+    // row's selected count is within 1.5x of their mean (workgroup 0 records the choice
+    // here for the merge); null otherwise
+    int32_t* ws_unsplit;
     int32_t qpos0[CA_MAX_BATCH];     // absolute position of each request's query row 0
     int32_t nkb[CA_MAX_BATCH];       // valid logical blocks of each request
     int32_t sp[CA_MAX_BATCH];        // splits of each request's block lists
@@ -128,13 +132,62 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     constexpr int BM = 32 * NW;
     __shared__ __attribute__((aligned(16))) uint8_t smem[kStages * kStageBytes];  // [stage]: K rows, then V rows
 
+    // Ragged launches whose row tiles fill 3/4 of the CUs: one round of row tiles is enough
+    // when the rows' selected counts are even, so the items of the other splits have nothing
+    // to do.  Every workgroup derives the same choice from the counts (wave 0, the flag through
+    // LDS before the stages are used; workgroup 0 records it for the merge).
+    int unsplit = 0;
+    if (kTab && p.ws_unsplit) {
+        volatile int* flag = reinterpret_cast<volatile int*>(smem);
+        if (threadIdx.x < 64) {
+            const int rows = p.s.B * p.s.Hkv;
+            int64_t sum = 0;
+            int mx = 0;
+            for (int r = threadIdx.x; r < rows; r += 64) {
+                const int c = min(max(p.counts[r], 0), p.s.cap);
+                sum += c;
+                mx = max(mx, c);
+            }
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) {
+                sum += __shfl_xor(sum, o, 64);
+                mx = max(mx, __shfl_xor(mx, o, 64));
+            }
+            if (threadIdx.x == 0) {
+                const int even = 2 * (int64_t)mx * rows <= 3 * sum ? 1 : 0;  // max <= 1.5 x mean
+                *flag = even;
+                if (blockIdx.x == 0) *p.ws_unsplit = even;
+            }
+        }
+        __syncthreads();
+        // uniform by construction; readfirstlane tells the compiler, which keeps the block-id
+        // and table reads that depend on it scalar (vector loads would wait behind the DMA)
+        unsplit = __builtin_amdgcn_readfirstlane(*flag);
+        __syncthreads();
+    }
+
     // workgroup -> (XCD x, k-th work item of x) -> (KV row, row tile, split)
     const int L = blockIdx.x;
     const int x = L & 7;
     int k = L >> 3;
     const Shape& s = p.s;
     int row, b, split, tile;
-    if (p.use_rows) {
+    if (p.use_rows && kTab && p.ws_unsplit) {
+        // split-major order on the XCD (its units are whole rows with one split count): the
+        // items of split 0 of every unit first, so an unsplit launch dispatches its working
+        // items first and the idle ones after them
+        const int i0 = p.xoff[x];
+        const int per = (p.xoff[x + 1] - i0) * p.ntiles;  // items of one split on this XCD
+        if (per == 0) return;
+        const int sidx = k / per;
+        const int kk = k - sidx * per;
+        const int i = i0 + kk / p.ntiles;
+        if (sidx >= p.xcnt[i]) return;
+        row = p.xrow[i];
+        b = row / s.Hkv;
+        split = p.xlo[i] + sidx;
+        tile = kk - (kk / p.ntiles) * p.ntiles;
+    } else if (p.use_rows) {
         int i = p.xoff[x];
         const int iend = p.xoff[x + 1];
         for (; i < iend; ++i) {
@@ -159,7 +212,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         tile = local / p.sp[b];
     }
     const int hk = row - b * s.Hkv;
-    const int nsplit = p.sp[b];
+    int nsplit = p.sp[b];
+    if (unsplit) {
+        if (split != 0) return;
+        nsplit = 1;
+    }
     const int G = s.G;
     const int qpos0 = p.qpos0[b];  // query row t sits at absolute position qpos0 + t
     const int nkb = p.nkb[b];      // valid logical block ids are [0, nkb)
@@ -455,6 +512,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnParams p) {
     const int hk = row - b * s.Hkv;
     const int nsplit = p.sp[b];
     if (nsplit == 1) return;  // the attention kernel wrote this request's rows directly
+    if (p.ws_unsplit && *p.ws_unsplit) return;  // so it did for every row of an unsplit launch
     const int t = r / s.G;
     const int g = r - t * s.G;
     // lane holds splits lane and lane + 32
@@ -806,6 +864,7 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
     //  - dense decode with more rows runs attn_fwd_kernel with the prefill sizing and up to
     //    64 splits.
     const bool dec = attn_uses_decode_kernel(s, dense);
+    plan->may_unsplit = 0;
     const int slots = dec ? 256 : 512;
     const int min_blocks = dec ? 32 : 16;
     const int max_splits = dense ? kMaxDecodeSplits : kMaxPrefillSplits;
@@ -837,6 +896,10 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
         forced = min(forced, max(1, nkb_max / min_blocks));
         forced = max(1, min(forced, max_splits));
         if (same_len && units * 4 >= 3 * 256) forced = 1;
+        // ragged batches with that many row tiles: the kernel decides from the selected
+        // counts (even counts: one round of unsplit tiles; config 4 at 20 % keep 278-281 vs
+        // 293-295 us split, while its dense tables need the split, 2.1 vs 3.2 ms)
+        plan->may_unsplit = !same_len && units * 4 >= 3 * 256 && forced > 1;
     }
     plan->max = 1;
     plan->off[0] = 0;
@@ -872,7 +935,8 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
     for (int b = 1; b < s.B; ++b) same_len = same_len && nkb[b] == nkb[0];
     int nunits = 0;
     for (int r = 0; r < rows; ++r) nunits += plan->s[r / s.Hkv];
-    const bool split_units = (rows % 8 != 0 || !same_len) && nunits <= kPlanRows;
+    // (a launch that may run unsplit keeps whole rows: each XCD's tiles then fit one round)
+    const bool split_units = (rows % 8 != 0 || !same_len) && nunits <= kPlanRows && !plan->may_unsplit;
     int unit_row[kPlanRows], unit_lo[kPlanRows], unit_cnt[kPlanRows];
     double unit_work[kPlanRows];  // blocks x row tiles the unit's items stream
     int units = 0;
@@ -967,7 +1031,8 @@ int attn_pick_splits(const Shape& s, const PastBlocks& pb, const int32_t* kv_len
 int64_t attn_workspace_bytes(const Shape& s, int num_splits) {
     if (num_splits <= 1) return 0;
     const int64_t rows_all = (int64_t)s.B * s.Hkv * s.Lq * s.G;
-    return (int64_t)num_splits * rows_all * (128 + 1) * (int64_t)sizeof(float);
+    // partials (128 values + log2-LSE per split and packed row), then the unsplit flag
+    return (int64_t)num_splits * rows_all * (128 + 1) * (int64_t)sizeof(float) + 16;
 }
 
 hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
@@ -1006,6 +1071,9 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     const int64_t rows_all = (int64_t)a.s.B * a.s.Hkv * p.rows_total;
     p.ws_o = plan.max > 1 ? static_cast<float*>(a.workspace) : nullptr;
     p.ws_lse = plan.max > 1 ? p.ws_o + (int64_t)plan.max * rows_all * 128 : nullptr;
+    p.ws_unsplit = plan.max > 1 && plan.may_unsplit && a.table
+                       ? reinterpret_cast<int32_t*>(p.ws_lse + (int64_t)plan.max * rows_all)
+                       : nullptr;
     if (a.table)
         hipLaunchKernelGGL((attn_fwd_kernel<kNW, true>), dim3(p.per_xcd * 8), dim3(kNW * 64), 0, stream, p);
     else if (attn_uses_decode_kernel(a.s, true))

@@ -105,7 +105,8 @@ struct SplitPlan {
     int32_t off[CA_MAX_BATCH + 1];
     int max;
     int use_rows;
-    int per_xcd;  // work items per XCD (grid = 8 * per_xcd)
+    int per_xcd;      // work items per XCD (grid = 8 * per_xcd)
+    int may_unsplit;  // the kernel drops the splits when the rows' selected counts are even
     uint16_t xrow[kPlanRows];  // placement units: a row and a range of its splits
     uint8_t xlo[kPlanRows];    // first split of the unit
     uint8_t xcnt[kPlanRows];   // splits in the unit

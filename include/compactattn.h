@@ -279,7 +279,8 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
  * count for the launch (ca_attn_pick_splits) with at least ~16 blocks per split: about 256
  * work items (row tiles x splits, one per CU) when all requests have one length, 1 when
  * their row tiles alone fill three quarters of the 256 CUs, and about 512 for ragged
- * batches.  The work is placed on the 8 XCDs in units: whole KV rows (longest first) when
+ * batches (a ragged launch whose row tiles fill three quarters of the CUs runs unsplit when
+ * its rows' selected counts are within 1.5x of their mean: the kernel decides from counts).  The work is placed on the 8 XCDs in units: whole KV rows (longest first) when
  * the requests have one length and the rows divide over the XCDs, otherwise single splits
  * of each row dealt round-robin request by request.  More than one split needs a workspace
  * of ca_attn_workspace_size(dims, past, num_splits) bytes.

@@ -90,7 +90,8 @@ def test_layout_and_workspace_validation():
     assert args(_seq(), _kv(), 17, None, 0) == _hip.CA_ERR_INVALID
     assert args(_seq(), _kv(), 2, None, 0) == _hip.CA_ERR_WORKSPACE
     need = lib.ca_attn_workspace_size(ctypes.byref(d), _past(0), 2)
-    assert need == 2 * 1 * 2 * 128 * 4 * 129 * 4  # splits * B*Hkv * Lq*G rows * 129 floats
+    # splits * B*Hkv * Lq*G rows * 129 floats, then a 16-byte flag slot
+    assert need == 2 * 1 * 2 * 128 * 4 * 129 * 4 + 16
     assert args(_seq(), _kv(), 2, FAKE, need - 1) == _hip.CA_ERR_WORKSPACE
     assert lib.ca_attn_pick_splits(ctypes.byref(d), _past(0)) >= 1
 
@@ -125,7 +126,7 @@ def test_decode_layout_and_workspace_validation():
     assert call(_seq(), 4, None, 0) == _hip.CA_ERR_WORKSPACE
     assert call(_seq(), 0, None, 0) == _hip.CA_ERR_WORKSPACE  # a 100-block row is split by the plan
     need = lib.ca_attn_decode_workspace_size(ctypes.byref(d), kv, 4)
-    assert need == 4 * 2 * 2 * (1 * 4) * 129 * 4  # splits * B*Hkv * Lq*G rows * 129 floats
+    assert need == 4 * 2 * 2 * (1 * 4) * 129 * 4 + 16  # splits * B*Hkv * Lq*G rows * 129 floats + flag
     assert call(_seq(), 4, FAKE, need - 1) == _hip.CA_ERR_WORKSPACE
     assert lib.ca_attn_decode_workspace_size(ctypes.byref(d), kv, 0) > 0
     assert lib.ca_attn_decode_workspace_size(ctypes.byref(d), kv, 65) < 0
