@@ -172,10 +172,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     int k = L >> 3;
     const Shape& s = p.s;
     int row, b, split, tile;
-    if (p.use_rows && kTab && p.ws_unsplit) {
-        // split-major order on the XCD (its units are whole rows with one split count): the
-        // items of split 0 of every unit first, so an unsplit launch dispatches its working
-        // items first and the idle ones after them
+    if (p.use_rows && kTab && unsplit) {
+        // an unsplit launch takes the XCD's items split-major (its units are whole rows with
+        // one split count): the items of split 0 of every unit first, so the working items are
+        // dispatched first and the idle ones after them (interleaved, the idle items held the
+        // working ones back: 510 vs 290 us on config 4); a split launch keeps the unit-major
+        // order below, which runs a long row's items before a short row's
         const int i0 = p.xoff[x];
         const int per = (p.xoff[x + 1] - i0) * p.ntiles;  // items of one split on this XCD
         if (per == 0) return;
