@@ -17,7 +17,7 @@ import oracle
 from compactattention_amd import ops
 from compactattention_amd.synthetic import make_chunk, rope_tables
 
-from .util import bits, f32, float_bits_equal, pack_rowmask, unpack_rowmask
+from .util import bits, f32, float_bits_equal, pack_rowmask, torch_reference_check, unpack_rowmask
 
 pytestmark = pytest.mark.gpu
 
@@ -481,6 +481,45 @@ def test_attention_ragged_split_plan(gpu):
     being split down to a few blocks) through the LSE merge."""
     _print_case(test="attention_ragged_plan")
     _attn_case(gpu, [64 * 16, 64 * 60, 64 * 120, 64 * 200], 128, 8, 2, "heads_first", 0, 0.3, seed=43)
+
+
+@pytest.mark.parametrize("even", [True, False])
+def test_attention_ragged_unsplit_choice(gpu, even):
+    """A ragged launch with enough row tiles (4 requests x 2 KV rows x 24 tiles of 256 query
+    rows) that the kernel picks between its split plan and one unsplit round from the
+    selected counts: every row selecting the same number of blocks runs unsplit; dense
+    tables over pasts of 16..128 blocks (largest count above 1.5x the mean) keep the
+    split and the LSE merge.  The choice is read from the workspace's last 16 bytes, and
+    the result is checked against the fp32 torch reference and against num_splits=1."""
+    _print_case(test="attention_ragged_unsplit", even=even)
+    past_tok, Lq, Hq, Hkv = [64 * 16, 64 * 32, 64 * 64, 64 * 128], 768, 16, 2
+    B, qb = len(past_tok), Lq // 64
+    ch = make_chunk(past_tok, Lq, Hq, Hkv, seed=47 + even)
+    cap, P = ch.kv_cap, ch.past_blocks
+    assert ops.attn_pick_splits(P, Lq, Hq, Hkv, cap) > 1
+    if even:  # 16 past blocks on every row
+        g = torch.Generator().manual_seed(48)
+        keep_kv = torch.zeros((B, Hkv, cap), dtype=torch.uint8)
+        for b in range(B):
+            for h in range(Hkv):
+                keep_kv[b, h, torch.randperm(P[b], generator=g)[:16]] = 1
+        table, counts = ops.compact_keep_kv(keep_kv.to(gpu), P, Lq, Hq, cap)
+    else:
+        table, counts = ops.dense_table(P, Lq, Hq, Hkv, cap, gpu)
+    cnt = counts.cpu()
+    assert (2 * int(cnt.max()) * B * Hkv <= 3 * int(cnt.sum())) == even
+    qg, kg, vg = ch.q.to(gpu), ch.k.to(gpu), ch.v.to(gpu)
+    K, V = ops.KV.heads_first(kg), ops.KV.heads_first(vg)
+    scale = 1.0 / math.sqrt(128)
+    need = ops.attn_workspace_bytes(P, Lq, Hq, Hkv, cap)
+    ws = torch.full((need,), 0x7F, dtype=torch.uint8, device=gpu)
+    out, lse = ops.attn_fwd(qg, K, V, table, counts, P, scale, cap, Hkv, with_lse=True, workspace=ws)
+    torch.cuda.synchronize()
+    assert int(ws[need - 16:need - 12].cpu().view(torch.int32)[0]) == int(even)
+    torch_reference_check(out, qg, kg, vg, P, table, counts, scale, lse=lse)
+    one = ops.attn_fwd(qg, K, V, table, counts, P, scale, cap, Hkv, num_splits=1)
+    err = (out.float() - one.float()).abs()
+    assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
 
 
 def test_attention_all_selected_equals_dense(gpu):
