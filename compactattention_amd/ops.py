@@ -125,6 +125,8 @@ class KV:
     layout: KvLayout
     page_table: Optional[torch.Tensor] = None
     tokens: Optional[int] = None  # token capacity of a contiguous layout (None when paged)
+    batch: Optional[int] = None   # requests of a contiguous layout (None when paged)
+    heads: Optional[int] = None   # KV heads of a contiguous layout (None when paged)
 
     @staticmethod
     def seq_first(t: torch.Tensor) -> "KV":
@@ -133,7 +135,7 @@ class KV:
         if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
             raise ValueError("seq-first KV must be [B, K, Hkv, 128] with a contiguous last dim")
         return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(2), BLOCK * t.stride(1), t.stride(1), None, 0,
-                              0), tokens=t.shape[1])
+                              0), tokens=t.shape[1], batch=t.shape[0], heads=t.shape[2])
 
     @staticmethod
     def heads_first(t: torch.Tensor) -> "KV":
@@ -142,7 +144,7 @@ class KV:
         if t.dim() != 4 or t.shape[-1] != HEAD_DIM or t.stride(-1) != 1:
             raise ValueError("heads-first KV must be [B, Hkv, K, 128] with a contiguous last dim")
         return KV(t, KvLayout(t.data_ptr(), t.stride(0), t.stride(1), BLOCK * t.stride(2), t.stride(2), None, 0,
-                              0), tokens=t.shape[2])
+                              0), tokens=t.shape[2], batch=t.shape[0], heads=t.shape[1])
 
     @staticmethod
     def paged(pool: torch.Tensor, page_table: torch.Tensor) -> "KV":
@@ -156,18 +158,23 @@ class KV:
         return KV(pool, KvLayout(pool.data_ptr(), 0, 0, pool.stride(0), pool.stride(1), page_table.data_ptr(),
                                  page_table.stride(0), pool.shape[0]), page_table)
 
-    def check_blocks(self, name: str, batch_rows: int, blocks: int, tokens: Optional[int] = None) -> None:
-        """Raise unless this layout covers ``blocks`` logical blocks of each of ``batch_rows``
-        rows: page-table columns, or for a contiguous cache whole 64-token blocks (``tokens``
-        tokens instead when the kernel's reads stop at that length)."""
+    def check_blocks(self, name: str, batch: int, heads: int, blocks: int, tokens: Optional[int] = None) -> None:
+        """Raise unless this layout covers ``blocks`` logical blocks of each of the ``batch`` x
+        ``heads`` KV rows: page-table rows and columns, or for a contiguous cache its requests,
+        heads and whole 64-token blocks (``tokens`` tokens instead when the kernel's reads stop
+        at that length)."""
         need = BLOCK * blocks if tokens is None else tokens
+        if self.batch is not None and (self.batch < batch or self.heads < heads):
+            raise ValueError(f"{name} cache holds {self.batch} requests x {self.heads} KV heads; the call "
+                             f"addresses {batch} x {heads}")
         if self.tokens is not None and self.tokens < need:
             raise ValueError(f"{name} cache holds {self.tokens} tokens; the call addresses {blocks} blocks "
                              f"({need} tokens)")
         if self.page_table is not None:
-            if self.page_table.shape[0] < batch_rows or self.page_table.shape[1] < blocks:
+            rows = batch * heads
+            if self.page_table.shape[0] < rows or self.page_table.shape[1] < blocks:
                 raise ValueError(f"{name} page_table {tuple(self.page_table.shape)} does not cover "
-                                 f"[{batch_rows}, {blocks}]")
+                                 f"[{rows}, {blocks}]")
 
 
 def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Optional[KV], v_cache: Optional[KV],
@@ -188,7 +195,7 @@ def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Opti
     blocks = max(int(p) for p in past_blocks) + Lq // BLOCK  # highest block written + 1
     for name, kv in (("k", k_cache), ("v", v_cache)):
         if kv is not None:
-            kv.check_blocks(name, B * Hkv, blocks)
+            kv.check_blocks(name, B, Hkv, blocks)
     if kmean is not None:
         _need_cuda("kmean", kmean, torch.float32)
         if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
@@ -250,8 +257,8 @@ def cache_fill_pool_query(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV,
     d = make_dims(B, Lq, Hq, Hkv, kv_cap)
     kn, vn, ql = seq_layout(k_new, "k_new"), seq_layout(v_new, "v_new"), seq_layout(q, "q")
     blocks = max(int(p) for p in past_blocks) + Lq // BLOCK
-    k_cache.check_blocks("k", B * Hkv, blocks)
-    v_cache.check_blocks("v", B * Hkv, blocks)
+    k_cache.check_blocks("k", B, Hkv, blocks)
+    v_cache.check_blocks("v", B, Hkv, blocks)
     _need_cuda("kmean", kmean, torch.float32)
     if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
         raise ValueError("kmean must be contiguous [B*Hkv, kv_cap, 128] fp32")
@@ -476,6 +483,8 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
     ql = seq_layout(q, "q")
     if out is None:
         out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape):
+        raise ValueError(f"out {tuple(out.shape)} must have q's shape {tuple(q.shape)}")
     ol = seq_layout(out, "out")
     _need_cuda("table", table, torch.int32)
     _need_cuda("counts", counts, torch.int32)
@@ -485,7 +494,7 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
         raise ValueError("counts must hold B*Hkv entries")
     blocks = max(int(p) for p in past_blocks) + Lq // BLOCK  # blocks a row's table may name
     for name, kv in (("k", k), ("v", v)):
-        kv.check_blocks(name, B * num_kv_heads, blocks)
+        kv.check_blocks(name, B, num_kv_heads, blocks)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     pa = past_array(past_blocks)
     # num_splits = 0 hands the choice to the library
@@ -525,13 +534,14 @@ def attn_decode(q: torch.Tensor, k: KV, v: KV, kv_len: Sequence[int], scale: flo
     ql = seq_layout(q, "q")
     if out is None:
         out = torch.empty_like(q)
+    elif tuple(out.shape) != tuple(q.shape):
+        raise ValueError(f"out {tuple(out.shape)} must have q's shape {tuple(q.shape)}")
     ol = seq_layout(out, "out")
-    # the kernel moves whole 64-token blocks: contiguous caches must hold the last one entirely
     # the kernel's buffer ranges end at each request's kv_len: a contiguous cache needs those
     # tokens only, a paged one a page for every block they touch
     max_len = max(int(x) for x in kv_len)
     for name, kv in (("k", k), ("v", v)):
-        kv.check_blocks(name, B * num_kv_heads, (max_len + BLOCK - 1) // BLOCK, tokens=max_len)
+        kv.check_blocks(name, B, num_kv_heads, (max_len + BLOCK - 1) // BLOCK, tokens=max_len)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     ka = past_array(kv_len)
     need = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), ka, int(num_splits))

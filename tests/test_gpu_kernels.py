@@ -643,3 +643,31 @@ def test_decode_cache_ending_at_kv_len(gpu):
     assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
     with pytest.raises(ValueError, match="holds 100 tokens"):
         ops.attn_decode(q.to(gpu), K, V, [101], 0.1, 2, 2)
+
+
+def test_host_checks_cover_kv_rows_and_out(gpu):
+    """Caches with fewer requests or KV heads than the call addresses, and outputs of another
+    shape, are refused on the host before any launch."""
+    _print_case(test="host_checks")
+    q = torch.zeros((2, 64, 4, 128), dtype=torch.bfloat16, device=gpu)
+    kc = torch.zeros((1, 2, 128, 128), dtype=torch.bfloat16, device=gpu)
+    K = ops.KV.heads_first(kc)
+    table, counts = ops.dense_table([1, 1], 64, 4, 2, 2, gpu)
+    with pytest.raises(ValueError, match="1 requests x 2 KV heads"):
+        ops.attn_fwd(q, K, K, table, counts, [1, 1], 0.1, 2, 2)
+    with pytest.raises(ValueError, match="1 requests x 2 KV heads"):
+        ops.attn_decode(q[:, :1], K, K, [100, 100], 0.1, 2, 2)
+    kc2 = torch.zeros((2, 128, 1, 128), dtype=torch.bfloat16, device=gpu)  # seq-first, one head
+    with pytest.raises(ValueError, match="2 requests x 1 KV heads"):
+        ops.attn_fwd(q, ops.KV.seq_first(kc2), ops.KV.seq_first(kc2), table, counts, [1, 1], 0.1, 2, 2)
+    kn = torch.zeros((2, 64, 2, 128), dtype=torch.bfloat16, device=gpu)
+    kmean = torch.zeros((4, 2, 128), dtype=torch.float32, device=gpu)
+    with pytest.raises(ValueError, match="1 requests x 2 KV heads"):
+        ops.cache_fill(kn, kn, K, K, [1, 1], 2, kmean)
+    kb = torch.zeros((2, 2, 128, 128), dtype=torch.bfloat16, device=gpu)
+    KB = ops.KV.heads_first(kb)
+    with pytest.raises(ValueError, match="must have q's shape"):
+        ops.attn_fwd(q, KB, KB, table, counts, [1, 1], 0.1, 2, 2, out=q[:, :, :2])
+    with pytest.raises(ValueError, match="must have q's shape"):
+        ops.attn_decode(q[:, :1], KB, KB, [100, 100], 0.1, 2, 2, out=q[:1, :1])
+    torch.cuda.synchronize()
