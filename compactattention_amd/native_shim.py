@@ -128,7 +128,11 @@ def build_flashinfer_kv_indices_cuda_out(*, selected_block_indices: torch.Tensor
     ca_table_to_csr computes the same prefix sum on the device, and only kv_indices is written."""
     rows = selected_block_counts.shape[0]
     table = selected_block_indices[:, :kv_blocks]
-    if table.stride(1) != 1:
+    if table.shape[1] < kv_blocks:  # the kernel may read a row's first kv_blocks entries
+        padded = torch.zeros((rows, kv_blocks), dtype=table.dtype, device=table.device)
+        padded[:, :table.shape[1]] = table
+        table = padded
+    elif table.stride(1) != 1:
         table = table.contiguous()
     _, indices, _ = ops.table_to_csr(table, selected_block_counts, rows, 1, int(kv_blocks))
     n = min(kv_indices.numel(), indices.numel())

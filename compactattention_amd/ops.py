@@ -98,10 +98,14 @@ def _need_cuda(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
         raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
 
 
-def past_array(past_blocks: Sequence[int]):
+def past_array(past_blocks: Sequence[int], batch: Optional[int] = None):
+    """Per-request values (past blocks or kv_len) as the int32 host array the C-ABI reads
+    ``batch`` entries of."""
     vals = [int(x) for x in past_blocks]
     if not 1 <= len(vals) <= _hip.MAX_BATCH:
         raise ValueError(f"batch must be in [1, {_hip.MAX_BATCH}]")
+    if batch is not None and len(vals) != batch:
+        raise ValueError(f"{len(vals)} per-request values for a batch of {batch}")
     return (ctypes.c_int32 * len(vals))(*vals)
 
 
@@ -217,7 +221,7 @@ def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Opti
     check(_hip.lib().ca_cache_fill(ctypes.byref(d), ctypes.byref(kn), ctypes.byref(vn) if vn is not None else None,
                                    ctypes.byref(k_cache.layout) if k_cache is not None else None,
                                    ctypes.byref(v_cache.layout) if v_cache is not None else None,
-                                   past_array(past_blocks), _ptr(kmean), _ptr(gate_wk), _ptr(rope_cos),
+                                   past_array(past_blocks, d.batch), _ptr(kmean), _ptr(gate_wk), _ptr(rope_cos),
                                    _ptr(rope_sin), rope_rows, _ptr(kgate), _stream()))
 
 
@@ -238,7 +242,7 @@ def pool_query(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, gate_wq
             _need_cuda("rope_sin", rope_sin, torch.float32)
             rope_rows = rope_cos.shape[0]
     qhat = torch.empty((B, Hq, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
-    check(_hip.lib().ca_pool_query(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks), _ptr(gate_wq),
+    check(_hip.lib().ca_pool_query(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks, d.batch), _ptr(gate_wq),
                                    _ptr(rope_cos), _ptr(rope_sin), rope_rows, qhat.data_ptr(), _stream()))
     return qhat
 
@@ -265,7 +269,7 @@ def cache_fill_pool_query(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV,
     qhat = torch.empty((B, Hq, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
     check(_hip.lib().ca_cache_fill_pool_query(ctypes.byref(d), ctypes.byref(kn), ctypes.byref(vn),
                                               ctypes.byref(k_cache.layout), ctypes.byref(v_cache.layout),
-                                              past_array(past_blocks), kmean.data_ptr(), ctypes.byref(ql),
+                                              past_array(past_blocks, d.batch), kmean.data_ptr(), ctypes.byref(ql),
                                               qhat.data_ptr(), _stream()))
     return qhat
 
@@ -306,8 +310,8 @@ def gate_key_summaries(k_new: torch.Tensor, past_blocks: Sequence[int], kv_cap: 
         raise ValueError(f"kgate must be contiguous [B, {gh}, kv_cap, 128] fp32")
     rows = _rope_args(rope_cos, rope_sin)
     d = make_dims(B, Lq, Hq, Hkv, kv_cap)
-    check(_hip.lib().ca_gate_key_summaries(ctypes.byref(d), ctypes.byref(kn), past_array(past_blocks), int(pools),
-                                           gate_wk.data_ptr(), gh, _ptr(rope_cos), _ptr(rope_sin), rows,
+    check(_hip.lib().ca_gate_key_summaries(ctypes.byref(d), ctypes.byref(kn), past_array(past_blocks, d.batch),
+                                           int(pools), gate_wk.data_ptr(), gh, _ptr(rope_cos), _ptr(rope_sin), rows,
                                            kgate.data_ptr(), _stream()))
 
 
@@ -334,9 +338,9 @@ def gate_query_summaries(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: in
     rows = _rope_args(rope_cos, rope_sin)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     qhat = torch.empty((B, gh, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
-    check(_hip.lib().ca_gate_query_summaries(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks), int(pools),
-                                             _ptr(gate_wq), gh, _ptr(rope_cos), _ptr(rope_sin), rows, qhat.data_ptr(),
-                                             _stream()))
+    check(_hip.lib().ca_gate_query_summaries(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks, d.batch),
+                                             int(pools), _ptr(gate_wq), gh, _ptr(rope_cos), _ptr(rope_sin), rows,
+                                             qhat.data_ptr(), _stream()))
     return qhat
 
 
@@ -352,6 +356,8 @@ def score_select(qhat: torch.Tensor, khat: torch.Tensor, scale: float, rule: Rul
     _need_cuda("khat", khat, torch.float32)
     if not qhat.is_contiguous() or not khat.is_contiguous():
         raise ValueError("qhat and khat must be contiguous")
+    if qhat.dim() != 4 or qhat.shape[3] != HEAD_DIM:
+        raise ValueError(f"qhat must be [B, Hq, Qb, {HEAD_DIM}]")
     B, Hq, Qb, _ = qhat.shape
     if khat.numel() < B * num_kv_heads * kv_cap * HEAD_DIM:
         raise ValueError("khat smaller than [B*Hkv, kv_cap, 128]")
@@ -360,7 +366,8 @@ def score_select(qhat: torch.Tensor, khat: torch.Tensor, scale: float, rule: Rul
     scores = torch.empty((B, Hq, Qb, kv_cap), dtype=torch.float32, device=qhat.device)
     r = rule.to_c()
     check(_hip.lib().ca_score_select(ctypes.byref(d), qhat.data_ptr(), khat.data_ptr(), float(scale), ctypes.byref(r),
-                                     past_array(past_blocks), rowmask.data_ptr(), scores.data_ptr(), _stream()))
+                                     past_array(past_blocks, d.batch), rowmask.data_ptr(), scores.data_ptr(),
+                                     _stream()))
     return rowmask, (scores if with_scores else None)
 
 
@@ -386,8 +393,8 @@ def select_scores(scores: torch.Tensor, rule: Rule, past_blocks: Sequence[int], 
     rowmask = torch.empty((B, Hq, Qb, words_for(kv_cap)), dtype=torch.int32, device=scores.device)
     r = rule.to_c()
     check(_hip.lib().ca_select_scores(ctypes.byref(d), scores.data_ptr(), dtype, scores.stride(0), scores.stride(1),
-                                      scores.stride(2), ctypes.byref(r), past_array(past_blocks), rowmask.data_ptr(),
-                                      _stream()))
+                                      scores.stride(2), ctypes.byref(r), past_array(past_blocks, d.batch),
+                                      rowmask.data_ptr(), _stream()))
     return rowmask
 
 
@@ -395,6 +402,8 @@ def union_compact(rowmask: torch.Tensor, past_blocks: Sequence[int], num_kv_head
                   last_n_block: int = 0, want_keep_block: bool = False, want_keep_kv: bool = False):
     """rowmask [B,Hq,Qb,words] -> (table [B*Hkv, kv_cap] i32, counts [B*Hkv] i32, keep_block, keep_kv)."""
     _need_cuda("rowmask", rowmask, torch.int32)
+    if rowmask.dim() != 4 or rowmask.shape[3] != words_for(kv_cap) or not rowmask.is_contiguous():
+        raise ValueError(f"rowmask must be contiguous [B, Hq, Qb, {words_for(kv_cap)}] int32")
     B, Hq, Qb, _ = rowmask.shape
     d = make_dims(B, Qb * BLOCK, Hq, num_kv_heads, kv_cap)
     dev = rowmask.device
@@ -402,9 +411,9 @@ def union_compact(rowmask: torch.Tensor, past_blocks: Sequence[int], num_kv_head
     counts = torch.empty((B * num_kv_heads,), dtype=torch.int32, device=dev)
     keep_block = torch.empty((B, Hq, kv_cap), dtype=torch.uint8, device=dev) if want_keep_block else None
     keep_kv = torch.empty((B, num_kv_heads, kv_cap), dtype=torch.uint8, device=dev) if want_keep_kv else None
-    check(_hip.lib().ca_union_compact(ctypes.byref(d), rowmask.data_ptr(), int(last_n_block), past_array(past_blocks),
-                                      _ptr(keep_block), _ptr(keep_kv), table.data_ptr(), table.stride(0),
-                                      counts.data_ptr(), _stream()))
+    check(_hip.lib().ca_union_compact(ctypes.byref(d), rowmask.data_ptr(), int(last_n_block),
+                                      past_array(past_blocks, d.batch), _ptr(keep_block), _ptr(keep_kv),
+                                      table.data_ptr(), table.stride(0), counts.data_ptr(), _stream()))
     return table, counts, keep_block, keep_kv
 
 
@@ -420,7 +429,7 @@ def compact_keep_kv(keep_kv: torch.Tensor, past_blocks: Sequence[int], q_len: in
     d = make_dims(B, q_len, num_q_heads, Hkv, kv_cap)
     table = torch.empty((B * Hkv, kv_cap), dtype=torch.int32, device=keep_kv.device)
     counts = torch.empty((B * Hkv,), dtype=torch.int32, device=keep_kv.device)
-    check(_hip.lib().ca_compact_keep_kv(ctypes.byref(d), keep_kv.data_ptr(), past_array(past_blocks),
+    check(_hip.lib().ca_compact_keep_kv(ctypes.byref(d), keep_kv.data_ptr(), past_array(past_blocks, d.batch),
                                         table.data_ptr(), table.stride(0), counts.data_ptr(), _stream()))
     return table, counts
 
@@ -431,8 +440,8 @@ def dense_table(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv
     d = make_dims(B, q_len, num_q_heads, num_kv_heads, kv_cap)
     table = torch.empty((B * num_kv_heads, kv_cap), dtype=torch.int32, device=device)
     counts = torch.empty((B * num_kv_heads,), dtype=torch.int32, device=device)
-    check(_hip.lib().ca_dense_table(ctypes.byref(d), past_array(past_blocks), table.data_ptr(), table.stride(0),
-                                    counts.data_ptr(), _stream()))
+    check(_hip.lib().ca_dense_table(ctypes.byref(d), past_array(past_blocks, d.batch), table.data_ptr(),
+                                    table.stride(0), counts.data_ptr(), _stream()))
     return table, counts
 
 
@@ -444,8 +453,10 @@ def table_to_csr(table: torch.Tensor, counts: torch.Tensor, batch: int, num_kv_h
     _need_cuda("table", table, torch.int32)
     _need_cuda("counts", counts, torch.int32)
     rows = batch * num_kv_heads
-    if table.dim() != 2 or table.stride(1) != 1 or table.shape[0] < rows:
+    if table.dim() != 2 or table.stride(1) != 1 or table.shape[0] < rows or table.shape[1] < kv_cap:
         raise ValueError("table must be [B*Hkv, >= kv_cap] with contiguous rows")
+    if counts.numel() < rows:
+        raise ValueError("counts must hold B*Hkv entries")
     d = make_dims(batch, BLOCK, num_kv_heads, num_kv_heads, kv_cap)
     dev = table.device
     indptr = torch.empty((rows + 1,), dtype=torch.int32, device=dev)
@@ -459,7 +470,7 @@ def table_to_csr(table: torch.Tensor, counts: torch.Tensor, batch: int, num_kv_h
 def attn_workspace_bytes(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int, kv_cap: int,
                          num_splits: int = 0) -> int:
     d = make_dims(len(past_blocks), q_len, num_q_heads, num_kv_heads, kv_cap)
-    n = _hip.lib().ca_attn_workspace_size(ctypes.byref(d), past_array(past_blocks), int(num_splits))
+    n = _hip.lib().ca_attn_workspace_size(ctypes.byref(d), past_array(past_blocks, d.batch), int(num_splits))
     if n < 0:
         raise _hip.CaError(int(n), _hip.last_error())
     return int(n)
@@ -468,7 +479,7 @@ def attn_workspace_bytes(past_blocks: Sequence[int], q_len: int, num_q_heads: in
 def attn_pick_splits(past_blocks: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int,
                      kv_cap: int) -> int:
     d = make_dims(len(past_blocks), q_len, num_q_heads, num_kv_heads, kv_cap)
-    n = _hip.lib().ca_attn_pick_splits(ctypes.byref(d), past_array(past_blocks))
+    n = _hip.lib().ca_attn_pick_splits(ctypes.byref(d), past_array(past_blocks, d.batch))
     if n < 0:
         raise _hip.CaError(int(n), _hip.last_error())
     return int(n)
@@ -496,7 +507,7 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
     for name, kv in (("k", k), ("v", v)):
         kv.check_blocks(name, B, num_kv_heads, blocks)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
-    pa = past_array(past_blocks)
+    pa = past_array(past_blocks, d.batch)
     # num_splits = 0 hands the choice to the library
     need = _hip.lib().ca_attn_workspace_size(ctypes.byref(d), pa, int(num_splits))
     if need < 0:
@@ -514,7 +525,7 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
 def attn_decode_workspace_bytes(kv_len: Sequence[int], q_len: int, num_q_heads: int, num_kv_heads: int,
                                 kv_cap: int, num_splits: int = 0) -> int:
     d = make_dims(len(kv_len), q_len, num_q_heads, num_kv_heads, kv_cap)
-    n = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), past_array(kv_len), int(num_splits))
+    n = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), past_array(kv_len, d.batch), int(num_splits))
     if n < 0:
         raise _hip.CaError(int(n), _hip.last_error())
     return int(n)
@@ -543,7 +554,7 @@ def attn_decode(q: torch.Tensor, k: KV, v: KV, kv_len: Sequence[int], scale: flo
     for name, kv in (("k", k), ("v", v)):
         kv.check_blocks(name, B, num_kv_heads, (max_len + BLOCK - 1) // BLOCK, tokens=max_len)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
-    ka = past_array(kv_len)
+    ka = past_array(kv_len, d.batch)
     need = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), ka, int(num_splits))
     if need < 0:
         raise _hip.CaError(int(need), _hip.last_error())

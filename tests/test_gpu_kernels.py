@@ -670,4 +670,9 @@ def test_host_checks_cover_kv_rows_and_out(gpu):
         ops.attn_fwd(q, KB, KB, table, counts, [1, 1], 0.1, 2, 2, out=q[:, :, :2])
     with pytest.raises(ValueError, match="must have q's shape"):
         ops.attn_decode(q[:, :1], KB, KB, [100, 100], 0.1, 2, 2, out=q[:1, :1])
+    with pytest.raises(ValueError, match="1 per-request values for a batch of 2"):
+        ops.attn_fwd(q, KB, KB, table, counts, [1], 0.1, 2, 2)
+    rowmask = torch.zeros((2, 4, 1, 2), dtype=torch.int32, device=gpu)  # words_for(2) is 1
+    with pytest.raises(ValueError, match="rowmask must be contiguous"):
+        ops.union_compact(rowmask, [1, 1], 2, 2)
     torch.cuda.synchronize()
