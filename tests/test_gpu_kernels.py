@@ -483,6 +483,14 @@ def test_attention_ragged_split_plan(gpu):
     _attn_case(gpu, [64 * 16, 64 * 60, 64 * 120, 64 * 200], 128, 8, 2, "heads_first", 0, 0.3, seed=43)
 
 
+@pytest.mark.parametrize("layout", ["seq_first", "paged"])
+def test_attention_ragged_rows_not_dividing_xcds(gpu, layout):
+    """Nine KV rows (3 requests x 3 KV heads) of ragged lengths under the automatic plan:
+    single splits dealt over the 8 XCDs, against the fp64 oracle in two more layouts."""
+    _print_case(test="attention_ragged_9_rows", layout=layout)
+    _attn_case(gpu, [64 * 10, 64 * 57, 64 * 120], 128, 6, 3, layout, 0, 0.35, seed=45)
+
+
 @pytest.mark.parametrize("even", [True, False])
 def test_attention_ragged_unsplit_choice(gpu, even):
     """A ragged launch with enough row tiles (4 requests x 2 KV rows x 24 tiles of 256 query
