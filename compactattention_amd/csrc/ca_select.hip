@@ -244,9 +244,9 @@ __global__ __launch_bounds__(256) void chunk_summaries_kernel(Shape s, SeqAddr k
 // ---------------------------------------------------------------------------------------
 // Block logits: logits[(b*Hq + h)*Qb + qb][kb] = dot(qhat[b,h,qb], khat[b, h/G, kb]) * scale
 // for the causal kb <= P + qb.  The G*Qb query vectors of a KV group are contiguous in
-// qhat, so a workgroup takes a 64 (query vectors) x 64 (key blocks) tile of one group;
-// each thread owns a 4 x 4 register tile and every dot product is one sequential fma chain
-// over d = 0..127.
+// qhat, so a workgroup takes a 64 (query vectors) x KT (key blocks) tile of one group;
+// each thread owns a 4 x KT/16 register tile and every dot product is one sequential fma
+// chain over d = 0..127.
 constexpr int kPadRow = kD + 4;  // LDS row pitch (floats) for summary tiles
 
 // One workgroup computes a 64-row x KT-key tile of logits (KT = 32: twice the workgroups of
