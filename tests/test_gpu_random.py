@@ -153,3 +153,53 @@ def test_random_chunk_step(gpu, seed):
     assert err.mean() <= ATOL_MEAN, err.mean()
     lerr = np.abs(f32(lse) - ref_lse)
     assert lerr.max() <= 4e-3, lerr.max()
+
+
+@pytest.mark.parametrize("seed", list(range(24)))
+def test_random_decode_step(gpu, seed):
+    """Dense decode over whole caches of unaligned lengths: 1-4 requests, 1-8 query rows each
+    (the last positions of kv_len), G up to 16, three KV layouts, automatic and forced split
+    counts; slots past each kv_len hold NaN and must not reach the result."""
+    rng = np.random.default_rng(5000 + seed)
+    B = int(rng.integers(1, 5))
+    Hkv = int(rng.choice([1, 2, 4, 8]))
+    G = int(rng.choice([1, 2, 4, 7, 16]))
+    Hq = Hkv * G
+    Lq = int(rng.integers(1, 9))
+    kv_len = [int(x) for x in rng.integers(Lq, 4000, size=B)]
+    cap = (max(kv_len) + 63) // 64 + int(rng.integers(0, 3))
+    layout = str(rng.choice(["heads_first", "seq_first", "paged"]))
+    splits = int(rng.choice([0, 0, 1, 3, 7]))
+    print(f"case: random decode seed={seed} B={B} Hkv={Hkv} G={G} Lq={Lq} kv_len={kv_len} cap={cap} "
+          f"layout={layout} splits={splits}", flush=True)
+    g = torch.Generator().manual_seed(6000 + seed)
+    q = torch.randn((B, Lq, Hq, 128), generator=g).to(torch.bfloat16)
+    k = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16)
+    v = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16)
+    for b, n in enumerate(kv_len):
+        k[b, :, n:] = float("nan")
+        v[b, :, n:] = float("nan")
+    if layout == "heads_first":
+        K, V = ops.KV.heads_first(k.to(gpu)), ops.KV.heads_first(v.to(gpu))
+    elif layout == "seq_first":
+        K = ops.KV.seq_first(k.transpose(1, 2).contiguous().to(gpu))
+        V = ops.KV.seq_first(v.transpose(1, 2).contiguous().to(gpu))
+    else:
+        rows = B * Hkv
+        perm = torch.randperm(rows * cap, generator=g).to(torch.int32).view(rows, cap)
+        pool_k = torch.full((rows * cap, 64, 128), float("nan"), dtype=torch.bfloat16)
+        pool_v = torch.full_like(pool_k, float("nan"))
+        pool_k[perm.view(-1).long()] = k.reshape(rows * cap, 64, 128)
+        pool_v[perm.view(-1).long()] = v.reshape(rows * cap, 64, 128)
+        K, V = ops.KV.paged(pool_k.to(gpu), perm.to(gpu)), ops.KV.paged(pool_v.to(gpu), perm.to(gpu))
+    scale = 1.0 / math.sqrt(128)
+    out, lse = ops.attn_decode(q.to(gpu), K, V, kv_len, scale, cap, Hkv, with_lse=True, num_splits=splits)
+    torch.cuda.synchronize()
+    ref, ref_lse = oracle.attention_decode(bits(q), bits(k), bits(v), kv_len, scale, with_lse=True)
+    got = f32(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    assert err.max() <= ATOL_MAX, err.max()
+    assert err.mean() <= ATOL_MEAN, err.mean()
+    lerr = np.abs(f32(lse) - ref_lse)
+    assert lerr.max() <= 4e-3, lerr.max()
