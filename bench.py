@@ -680,7 +680,9 @@ def model_prefill(tokens, chunk, layers, dev, seer_only: bool = False):
     from compactattention_amd.prefill_sparse.llama import (SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaConfig,
                                                            SeerAttnLlamaFlashPrefillCompactAttnForCausalLM)
 
-    cfg = SeerAttnLlamaConfig(num_hidden_layers=layers, max_position_embeddings=max(tokens, 131072))
+    from compactattention_amd.synthetic import BASELINE_SEER
+
+    cfg = SeerAttnLlamaConfig(num_hidden_layers=layers, max_position_embeddings=max(tokens, 131072), **BASELINE_SEER)
     model = SeerAttnLlamaChunkedDenseForCausalLM(cfg, device=dev)
     model.init_weights(seed=1234)
     ids = synthetic_prompt(1, tokens, cfg.vocab_size, 1234 + 131072 * 104729, dev)

@@ -537,11 +537,18 @@ int ca_attn_fwd_noalloc(const ca_dims* dims, const ca_seq_layout* q, const ca_kv
     if ((rc = check_dims(dims, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
     if (num_splits < 0 || num_splits > ca::kMaxPrefillSplits)
         return fail(CA_ERR_INVALID, "num_splits=%d outside [0, %d]", num_splits, ca::kMaxPrefillSplits);
+    // num_splits = 0 passes through when the automatic count's partials fit the library's
+    // scratch array (ca_attn_fwd then plans exactly as for num_splits = 0, including the ragged
+    // launch's split-or-unsplit choice); otherwise the count is lowered until they fit and
+    // forced
     int splits = num_splits;
+    int forward = num_splits;
     if (splits == 0) {
-        // the automatic count, lowered until its partials fit the library's scratch array
         splits = ca::attn_pick_splits(s, pb, nullptr);
-        while (splits > 1 && ca::attn_workspace_bytes(s, splits) > (int64_t)CA_STATIC_SCRATCH_BYTES) --splits;
+        if (ca::attn_workspace_bytes(s, splits) > (int64_t)CA_STATIC_SCRATCH_BYTES) {
+            while (splits > 1 && ca::attn_workspace_bytes(s, splits) > (int64_t)CA_STATIC_SCRATCH_BYTES) --splits;
+            forward = splits;
+        }
     }
     const int64_t need = ca::attn_workspace_bytes(s, splits);
     if (need > (int64_t)CA_STATIC_SCRATCH_BYTES)
@@ -550,7 +557,7 @@ int ca_attn_fwd_noalloc(const ca_dims* dims, const ca_seq_layout* q, const ca_kv
                     (long long)CA_STATIC_SCRATCH_BYTES);
     void* ws = nullptr;
     if (need > 0 && (rc = scratch_for_stream(static_cast<hipStream_t>(stream), &ws)) != CA_OK) return rc;
-    return ca_attn_fwd(dims, q, k, v, table, table_stride, counts, past_blocks_host, scale, out, lse, splits, ws,
+    return ca_attn_fwd(dims, q, k, v, table, table_stride, counts, past_blocks_host, scale, out, lse, forward, ws,
                        need, stream);
 }
 

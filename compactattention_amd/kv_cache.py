@@ -15,7 +15,13 @@ Layout of one layer:
   - the page table: int32 ``[B*Hkv, blocks]`` (row = b*Hkv + h), logical block -> page id,
     kept on the device for the kernels and mirrored on the host, where pages are allocated;
   - block summaries by logical block: kmean ``[B, Hkv, blocks, 128]`` fp32 (FlashPrefill
-    scoring) and, with a gate, kgate ``[B, gate_heads, blocks, 128]`` fp32.
+    scoring) and, with a gate, kgate ``[B, gate_heads, blocks, 128]`` fp32.  ``kmean_blocks`` /
+    ``kgate_blocks`` count the leading blocks whose summaries are valid: decode appends write
+    no summaries, so a block that decode tokens complete has none until the next chunk append
+    recomputes its mean-K from the cached keys (the reference's FlashPrefill model recomputes
+    its mean-K cache when the token count disagrees, modeling_llama_flashprefill_compactattn.py:
+    128-147).  Gate-K summaries come from pre-RoPE keys the cache does not hold, so a chunk that
+    follows such a block raises (``require_kgate``).
 Pages are reference-counted: ``fork`` lets a request share another's pages, and a decode
 append into a shared, partly filled page copies it first.  Appends write the chunk's pages
 and summaries in place through the cache-fill kernel; nothing is ever re-copied.
@@ -105,6 +111,8 @@ class PagedKVCache:
         self.kmean = self._summary(num_kv_heads) if with_kmean else None
         self.kgate = self._summary(self.kgate_heads) if with_kgate else None
         self.length = 0  # tokens stored per request
+        self.kmean_blocks = 0  # leading blocks with a valid kmean
+        self.kgate_blocks = 0  # leading blocks with a valid kgate
 
     # -- layout ---------------------------------------------------------------------------
     def _summary(self, heads: int) -> torch.Tensor:
@@ -202,11 +210,18 @@ class PagedKVCache:
         if gate_wk is not None and (self.kgate is None or self.kgate_heads != Hkv):
             raise ValueError("cache built without a per-KV-head gate-K summary buffer")
         past = self.past_blocks
+        if gate_wk is not None:
+            self.require_kgate(past)
+        self.refresh_kmean(past)
         self._map(past, past + L // BLOCK)
         K, V = self.layouts()
         ops.cache_fill(k_new, v_new, K, V, [past] * B, self.cap, self.kmean, gate_wk=gate_wk, rope_cos=rope_cos,
                        rope_sin=rope_sin, kgate=self.kgate if gate_wk is not None else None)
         self.length += L
+        if self.kmean is not None:
+            self.kmean_blocks = self.past_blocks
+        if gate_wk is not None:
+            self.kgate_blocks = self.past_blocks
         return past
 
     def append_with_query_means(self, k_new: torch.Tensor, v_new: torch.Tensor,
@@ -224,11 +239,33 @@ class PagedKVCache:
         if self.kmean is None:
             raise ValueError("cache built without the mean-K summaries")
         past = self.past_blocks
+        self.refresh_kmean(past)
         self._map(past, past + L // BLOCK)
         K, V = self.layouts()
         qhat = ops.cache_fill_pool_query(k_new, v_new, K, V, [past] * B, self.cap, self.kmean, q)
         self.length += L
+        self.kmean_blocks = self.past_blocks
         return past, qhat
+
+    def refresh_kmean(self, upto: int) -> None:
+        """Write the mean-K of blocks [kmean_blocks, upto) from the cached keys (blocks that
+        decode appends completed), by the cache-fill kernel in summaries-only mode; the means
+        are the ones a chunk append of the same keys writes, bit for bit."""
+        if self.kmean is None or self.kmean_blocks >= upto:
+            return
+        b0 = self.kmean_blocks
+        idx = torch.from_numpy(np.ascontiguousarray(self._pt[:, b0:upto]).astype(np.int64)).to(self.device)
+        n = (upto - b0) * BLOCK
+        keys = self.pool.k[idx.reshape(-1)].view(self.batch, self.num_kv_heads, n, HEAD_DIM).transpose(1, 2)
+        ops.cache_fill(keys, None, None, None, [b0] * self.batch, self.cap, self.kmean)
+        self.kmean_blocks = upto
+
+    def require_kgate(self, past: int) -> None:
+        """A selecting chunk at ``past`` blocks needs gate-K summaries for every past block."""
+        if self.kgate is not None and self.kgate_blocks < past:
+            raise ValueError(f"gate-K summaries are missing for blocks [{self.kgate_blocks}, {past}): decode tokens "
+                             "completed them and the cache keeps no pre-RoPE keys to pool; prefill the rest of the "
+                             "sequence densely or start it again")
 
     def append_tokens(self, k_new: torch.Tensor, v_new: torch.Tensor) -> int:
         """Decode append: [B, L, Hkv, 128] bf16 K/V (any L) at the current length, which need
@@ -308,3 +345,5 @@ class PagedKVCache:
             self._pt[:] = -1
             self.page_table.fill_(-1)
         self.length = 0
+        self.kmean_blocks = 0
+        self.kgate_blocks = 0

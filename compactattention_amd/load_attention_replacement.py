@@ -111,7 +111,11 @@ def _build_seer_config(hf_config, *, variant: str, threshold: float, compactattn
         rms_norm_eps=float(hf_config.rms_norm_eps),
         rope_theta=_rope_theta(hf_config),
         max_position_embeddings=hf_config.max_position_embeddings,
+        # the reference sets both thresholds and no schedule (load_attention_replacement.py:136-144);
+        # no sink or local blocks: the Seer layer keeps the last keep_recent_blocks KV blocks
         seerattn_threshold=float(threshold),
+        seerattn_compactattn_threshold=float(threshold),
+        seerattn_compactattn_threshold_schedule=None,
         seerattn_compactattn_keep_recent_blocks=int(compactattn_keep_recent_blocks),
         seerattn_flashprefill_alpha=float(flashprefill_alpha),
         seerattn_flashprefill_block_size=int(flashprefill_block_size),
@@ -242,6 +246,7 @@ def load_llama_attention_replacement_model(
     model.config.seerattn_cache_layout = (
         "heads_first_flashprefill" if variant == "flashprefill_compactattn" else "heads_first_seer")
     model.compactattn_config = seer_cfg
+    model.compactattn_block_rope = block_rope
     return model
 
 

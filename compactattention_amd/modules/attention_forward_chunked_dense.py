@@ -10,15 +10,23 @@ block tables, and the HIP indexed MFMA attention reading K/V in place through th
 pack_impl / indexed_impl / cache_fill_backend are validated like the reference and then
 all map to that path.
 
+Selection (the reference's _build_keep_block_mask_chunked_fast_path + _build_kv_head_union_
+keep_block_mask, :559-683): a past block is kept for a Q head when some query block's gate score
+is strictly above the threshold, the last keep_recent_blocks KV blocks are forced (the current
+chunk's blocks, then the past blocks right before it when keep_recent_blocks exceeds the
+chunk's block count), the current chunk is always attended, and the KV group takes the union
+of its Q heads.  The threshold is a float or a tensor with one value per request (:383-393).
+
 Supported inputs (anything else raises ValueError): block_size 64, no padding in
-attention_mask, head_dim 128, bf16 Q/K/V on the GPU, scalar threshold.  A call whose q_len
-or kv_len is not a multiple of 64 selects for its block-aligned head and attends densely for
-its last q_len % 64 queries (all of them below 64 queries); such a chunk of 64 or more
-queries must start at a block boundary.
+attention_mask, head_dim 128, bf16 Q/K/V on the GPU.  A call whose q_len or kv_len is not a
+multiple of 64 selects for its block-aligned head and attends densely for its last q_len % 64
+queries (all of them below 64 queries); such a chunk of 64 or more queries must start at a
+block boundary.
 """
 from __future__ import annotations
 
-from typing import Dict, Optional, Tuple, Union
+import os
+from typing import Dict, List, Optional, Tuple, Union
 
 import torch
 
@@ -30,12 +38,64 @@ PACK_IMPLS = frozenset({"torch", "triton", "indexed_dense"})
 CACHE_FILL_BACKENDS = frozenset({"auto", "cuda", "triton"})
 
 
-def _effective_threshold(threshold: Union[float, torch.Tensor]) -> float:
+def _compactattn_effective_threshold(threshold: Union[float, torch.Tensor]) -> Union[float, torch.Tensor]:
+    """A tensor passes through; a float can be replaced by the
+    SEERATTN_DEBUG_COMPACTATTN_THRESHOLD_OVERRIDE environment value (reference :115-124)."""
     if isinstance(threshold, torch.Tensor):
-        if threshold.numel() != 1:
-            raise ValueError("per-request threshold tensors are not supported; pass a scalar")
-        return float(threshold.item())
+        return threshold
+    raw = os.environ.get("SEERATTN_DEBUG_COMPACTATTN_THRESHOLD_OVERRIDE")
+    if raw is not None:
+        try:
+            return float(raw)
+        except ValueError:
+            pass
     return float(threshold)
+
+
+def _compactattn_keep_recent_blocks(default: int) -> int:
+    """keep_recent_blocks, or the SEERATTN_DEBUG_COMPACTATTN_KEEP_RECENT_OVERRIDE environment value
+    (clamped at 0; reference :141-148)."""
+    raw = os.environ.get("SEERATTN_DEBUG_COMPACTATTN_KEEP_RECENT_OVERRIDE")
+    if raw is not None:
+        try:
+            return max(int(raw), 0)
+        except ValueError:
+            pass
+    return int(default)
+
+
+def keep_recent_local_blocks(keep_recent_blocks: int, q_blocks: int) -> int:
+    """Forcing the last keep_recent_blocks of the P + Qb KV blocks (reference :632-636) keeps the
+    Qb current blocks (always kept here) and, beyond them, the keep_recent_blocks - Qb past blocks
+    right before the chunk: the selection rule's local_blocks."""
+    return max(0, int(keep_recent_blocks) - int(q_blocks))
+
+
+def request_thresholds(threshold: Union[float, torch.Tensor], batch: int) -> List[float]:
+    """One threshold per request: a float or one-element tensor for all, or a 1-D tensor of
+    ``batch`` values (the reference broadcasts view(-1, 1, 1) over [B, H, Kb], :383-393)."""
+    if not isinstance(threshold, torch.Tensor):
+        return [float(threshold)] * batch
+    if threshold.dim() > 1:
+        raise ValueError(f"Expected scalar or 1D batch threshold tensor, got shape={tuple(threshold.shape)}")
+    vals = [float(x) for x in threshold.detach().float().cpu().reshape(-1).tolist()]
+    if len(vals) == 1:
+        return vals * batch
+    if len(vals) != batch:
+        raise ValueError(f"threshold tensor has {len(vals)} values for a batch of {batch}")
+    return vals
+
+
+def _full_width_scores(scores: torch.Tensor, kv_blocks: int) -> torch.Tensor:
+    """Gate scores over fewer than kv_blocks key blocks cover the last columns (the reference
+    right-aligns a short keep mask, _project_short_qhead_keep_block_to_kv_full_width,
+    :708-734); the missing leading columns read as -inf, which no threshold keeps."""
+    short = scores.shape[-1]
+    if short >= kv_blocks:
+        return scores
+    full = torch.full((*scores.shape[:-1], kv_blocks), float("-inf"), dtype=scores.dtype, device=scores.device)
+    full[..., kv_blocks - short:] = scores
+    return full
 
 
 def _validate_impls(pack_impl: str, indexed_impl: str, cache_fill_backend: str) -> None:
@@ -93,11 +153,13 @@ def chunked_prefill_column_dense_attention_forward(
     """Seer compactattn: keep KV block kb for Q head h iff max over the causal query blocks
     of attn_gate_score[b, h, qb, kb] > threshold (reference: _build_keep_block_mask /
     build_keep_past_fast, attention_forward_chunked_dense.py:352-403,559-638), force the
-    current chunk open, union over the GQA group, then attend over the selected blocks.
+    last keep_recent_blocks KV blocks and the current chunk open, union over the GQA group,
+    then attend over the selected blocks.
 
     block_attention_mask, when given, must be the standard causal block mask (the path
-    applies causality itself).  keep_recent_blocks forces the last KV blocks, which are the
-    current chunk's and therefore always kept."""
+    applies causality itself).  A threshold tensor holds one value per request; with it the
+    past columns' validity is the causal block mask here too (the reference's generic path
+    takes a top-left triangle when block_attention_mask is None)."""
     del attn_module, block_attention_mask
     if attn_gate_score is None:
         raise ValueError("attn_gate_score is required for chunked column-dense attention.")
@@ -106,7 +168,8 @@ def chunked_prefill_column_dense_attention_forward(
     if block_size <= 0:
         raise ValueError("block_size must be positive.")
     _validate_impls(pack_impl, indexed_impl, cache_fill_backend)
-    thr = _effective_threshold(threshold)
+    threshold = _compactattn_effective_threshold(threshold)
+    keep_recent_blocks = _compactattn_keep_recent_blocks(keep_recent_blocks)
     kv_len = k_hf.shape[2] if k_hf is not None else key_states.shape[1]
     num_kv_heads = k_hf.shape[1] if k_hf is not None else key_states.shape[2]
     if query_states.dim() == 4 and query_states.shape[1] != query_length:
@@ -134,6 +197,7 @@ def chunked_prefill_column_dense_attention_forward(
     check_attention_mask(attention_mask, geo.batch, kv_len)
     if keep_recent_blocks < 0:
         raise ValueError("keep_recent_blocks must be >= 0")
+    thresholds = request_thresholds(threshold, geo.batch)
     K, V = kv_layouts(key_states, value_states, k_hf, v_hf)
     timer = StageTimer(return_stats)
     P = [geo.past_blocks] * geo.batch
@@ -146,21 +210,33 @@ def chunked_prefill_column_dense_attention_forward(
                 attn_gate_score.shape[1] != sel_heads or attn_gate_score.shape[2] != geo.q_blocks:
             raise ValueError(f"attn_gate_score must be [B, {sel_heads}, {geo.q_blocks}, Kb], got "
                              f"{tuple(attn_gate_score.shape)}")
-        if attn_gate_score.shape[3] < geo.kv_cap:
-            raise ValueError(f"attn_gate_score has {attn_gate_score.shape[3]} key blocks, expected {geo.kv_cap}")
+        short = attn_gate_score.shape[3]
+        if short > geo.kv_cap:
+            raise ValueError(f"short keep_block width {short} exceeds expected KV blocks {geo.kv_cap}")
         scores = attn_gate_score if attn_gate_score.stride(-1) == 1 else attn_gate_score.contiguous()
         if scores.dtype not in (torch.float32, torch.bfloat16):
             scores = scores.float()
-        rule = ops.Rule(threshold=thr)
-        # kv-group-aware gates score per KV head: selection then runs with G = 1
-        rowmask = timer("col_select_mask_ms", lambda: ops.select_scores(
-            scores, rule, P, geo.num_kv_heads, geo.kv_cap, geo.q_len))
+        scores = _full_width_scores(scores, geo.kv_cap)
+        # the forced recent columns of a short score row stop at its first column
+        local = keep_recent_local_blocks(min(keep_recent_blocks, short), geo.q_blocks)
+
+        def select():
+            # kv-group-aware gates score per KV head: selection then runs with G = 1
+            if len(set(thresholds)) == 1:
+                return ops.select_scores(scores, ops.Rule(threshold=thresholds[0], local_blocks=local), P,
+                                         geo.num_kv_heads, geo.kv_cap, geo.q_len)
+            return torch.cat([ops.select_scores(scores[b:b + 1], ops.Rule(threshold=t, local_blocks=local), P[b:b + 1],
+                                                geo.num_kv_heads, geo.kv_cap, geo.q_len)
+                              for b, t in enumerate(thresholds)])
+
+        rowmask = timer("col_select_mask_ms", select)
         table, counts, _, _ = timer("col_union_table_ms", lambda: ops.union_compact(
             rowmask, P, geo.num_kv_heads, geo.kv_cap))
     out = timer("col_index_attn_ms", lambda: attend(query_states, K, V, table, counts, geo, softmax_scale))
     if not return_stats:
         return out, None
-    stats: Dict[str, float] = {"compactattn_version": COMPACTATTN_VERSION, "col_threshold": thr}
+    thr_stat = float(threshold) if not isinstance(threshold, torch.Tensor) else float(threshold.float().mean())
+    stats: Dict[str, float] = {"compactattn_version": COMPACTATTN_VERSION, "col_threshold": thr_stat}
     stats.update(timer.results())
     stats.update(table_stats(counts, geo, "col_"))
     return out, stats

@@ -17,6 +17,14 @@ BLOCK = 64
 HEAD_DIM = 128
 DEFAULT_SEED = 1234  # the reference harness default (eval/chunked_prefill/profile_attention_latency.py:421)
 
+# BASELINE configs 1 and 3's Seer selector as SeerAttnLlamaConfig fields: the AttnGate with
+# pooled Q and K both projected per head (Qavg_Kavg, force_double), softmax threshold 5e-3,
+# sink block 0 and the 2 local blocks before the chunk.  The reference's own layer has neither
+# sink nor local blocks (it forces the last keep_recent_blocks KV blocks); these two fields are
+# this build's extension for the benchmark rule.
+BASELINE_SEER = dict(seerattn_gate_type="Qavg_Kavg", seerattn_gate_force_double=True,
+                     seerattn_compactattn_threshold=5e-3, compactattn_sink_blocks=1, compactattn_local_blocks=2)
+
 
 @dataclass
 class ChunkInputs:

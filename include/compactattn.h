@@ -303,8 +303,9 @@ int ca_attn_fwd(const ca_dims* dims, const ca_seq_layout* q, const ca_kv_layout*
  * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation).
  * The split partials live in a library-owned device array of CA_STATIC_SCRATCH_BYTES that
  * each GPU the library runs on holds until the process ends (looked up on a device's first
- * call; the current device must be the stream's).  num_splits = 0 takes ca_attn_fwd's
- * automatic count lowered until its partials fit; a positive count whose partials
+ * call; the current device must be the stream's).  num_splits = 0 runs exactly as ca_attn_fwd
+ * with num_splits = 0 when the automatic count's partials fit the array; otherwise that count
+ * is lowered until they fit and used as a fixed count.  A positive count whose partials
  * (ca_attn_workspace_size) exceed the array fails with CA_ERR_LIMIT.  All calls on one GPU
  * share its array: calls that overlap on one GPU (other streams, other threads) race.
  */

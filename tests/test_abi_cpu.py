@@ -250,8 +250,10 @@ def test_python_entry_points_reject_bad_arguments():
         f(q, k[:, :600], k[:, :600], None, 128, attn_gate_score=gate, num_key_value_groups=4)
     with pytest.raises(ValueError, match="does not match query_states"):
         f(q[:, :100], k, k, None, 128, attn_gate_score=gate, num_key_value_groups=4)
-    with pytest.raises(ValueError, match="per-request threshold"):
+    with pytest.raises(ValueError, match="threshold tensor has 2 values for a batch of 1"):
         f(q, k, k, None, 128, attn_gate_score=gate, threshold=torch.zeros(2), num_key_value_groups=4)
+    with pytest.raises(ValueError, match="Expected scalar or 1D batch threshold tensor"):
+        f(q, k, k, None, 128, attn_gate_score=gate, threshold=torch.zeros((1, 1)), num_key_value_groups=4)
     with pytest.raises(ValueError, match="Either keep_block"):
         chunked_prefill_column_dense_attention_from_keep_block(q, k, k, None, None, 128, 0.1,
                                                                num_key_value_groups=4)

@@ -24,7 +24,8 @@ from compactattention_amd.modules.flashprefill_prefill import (flashprefill_comp
 from compactattention_amd.prefill_sparse.attn_gate import ATTNGATE_CLASSES
 from compactattention_amd.synthetic import make_chunk, rope_tables
 
-from .util import bits, f32, float_bits_equal, oracle_gate_summaries, ref_flashprefill_tables
+from .util import (bits, f32, float_bits_equal, oracle_gate_summaries, ref_flashprefill_tables, ref_seer_tables,
+                   spy_union_compact, torch_reference_check)
 
 pytestmark = pytest.mark.gpu
 
@@ -70,6 +71,96 @@ def test_seer_forward_threshold(gpu, use_hf, kv_group_aware):
     _, _, table, counts = oracle.union_compact(keep, Hkv, P)
     assert stats["col_selected_blocks"] == counts.sum()
     _check_attention(out, ch, table, counts)
+
+
+@pytest.mark.parametrize("Qb,keep_recent", [(1, 2), (1, 4), (16, 2), (16, 4), (4, 9)])
+@pytest.mark.parametrize("kv_group_aware", [False, True])
+def test_seer_entry_reference_rule(gpu, monkeypatch, Qb, keep_recent, kv_group_aware):
+    """The Seer entry's tables equal the reference's selection (a torch restatement of
+    _build_keep_block_mask_chunked_fast_path + _build_kv_head_union_keep_block_mask,
+    attention_forward_chunked_dense.py:559-683) bit for bit: strict threshold over the query
+    blocks, the last keep_recent_blocks KV columns forced -- past blocks too once
+    keep_recent_blocks exceeds the chunk's Qb blocks -- and the GQA union; then every query row
+    of the output against an fp32 torch attention over those tables."""
+    _print_case(test="seer_entry_reference_rule", Qb=Qb, keep_recent=keep_recent, kv_group_aware=kv_group_aware)
+    Hq, Hkv, Lq, past = 8, 2, 64 * Qb, 64 * 44
+    ch = make_chunk([past, past], Lq, Hq, Hkv, seed=30 + Qb)
+    P, cap = ch.past_blocks, ch.kv_cap
+    Hs = Hkv if kv_group_aware else Hq
+    g = torch.Generator().manual_seed(31)
+    logits = torch.randn((2, Hs, Qb, cap), generator=g) * 2.5
+    causal = torch.arange(cap)[None, :] <= (P[0] + torch.arange(Qb))[:, None]
+    gate = torch.softmax(logits.masked_fill(~causal, float("-inf")), dim=-1)
+    thr = 0.03
+    calls = spy_union_compact(monkeypatch)
+    out, stats = chunked_prefill_column_dense_attention_forward(
+        ch.q.to(gpu), _seq_first(ch.k).to(gpu), _seq_first(ch.v).to(gpu), None, Lq, softmax_scale=SCALE,
+        attn_gate_score=gate.to(gpu), threshold=thr, keep_recent_blocks=keep_recent, num_key_value_groups=Hq // Hkv,
+        attn_gate_is_kv_group_aware=kv_group_aware, pack_impl="indexed_dense", return_stats=True,
+        k_hf=ch.k.to(gpu), v_hf=ch.v.to(gpu))
+    ref_table, ref_counts = ref_seer_tables(gate.numpy(), P, Hkv, thr, keep_recent, kv_group_aware=kv_group_aware)
+    assert len(calls) == 1
+    table, counts = (t.cpu().numpy() for t in calls[0])
+    assert np.array_equal(counts, ref_counts)
+    assert np.array_equal(table, ref_table)
+    assert stats["col_selected_blocks"] == ref_counts.sum()
+    assert ref_counts.min() < P[0] + Qb, "the case should drop blocks"
+    if keep_recent > Qb:  # the forced past blocks right before the chunk
+        for r in range(2 * Hkv):
+            assert set(range(P[0] - (keep_recent - Qb), P[0])) <= set(ref_table[r, :ref_counts[r]].tolist())
+    torch_reference_check(out, ch.q.to(gpu), ch.k.to(gpu), ch.v.to(gpu), P, calls[0][0], calls[0][1], SCALE)
+
+
+def test_seer_entry_per_request_threshold(gpu, monkeypatch):
+    """A 1-D threshold tensor selects each request with its own value (the reference's
+    view(-1, 1, 1) broadcast, attention_forward_chunked_dense.py:383-393); the tables equal the
+    restatement with per-request thresholds, and request 1's equal a scalar call's with its value."""
+    _print_case(test="seer_entry_per_request_threshold")
+    Hq, Hkv, Lq, past = 8, 2, 256, 64 * 30
+    ch = make_chunk([past, past], Lq, Hq, Hkv, seed=41)
+    P, cap = ch.past_blocks, ch.kv_cap
+    g = torch.Generator().manual_seed(42)
+    logits = torch.randn((2, Hq, Lq // 64, cap), generator=g) * 2.5
+    causal = torch.arange(cap)[None, :] <= (P[0] + torch.arange(Lq // 64))[:, None]
+    gate = torch.softmax(logits.masked_fill(~causal, float("-inf")), dim=-1)
+    thr = torch.tensor([0.01, 0.08])
+    calls = spy_union_compact(monkeypatch)
+    args = (ch.q.to(gpu), _seq_first(ch.k).to(gpu), _seq_first(ch.v).to(gpu), None, Lq)
+    kw = dict(softmax_scale=SCALE, attn_gate_score=gate.to(gpu), num_key_value_groups=Hq // Hkv)
+    chunked_prefill_column_dense_attention_forward(*args, threshold=thr.to(gpu), **kw)
+    ref_table, ref_counts = ref_seer_tables(gate.numpy(), P, Hkv, thr.tolist(), 2)
+    table, counts = (t.cpu().numpy() for t in calls[0])
+    assert np.array_equal(counts, ref_counts) and np.array_equal(table, ref_table)
+    assert ref_counts[:Hkv].sum() > ref_counts[Hkv:].sum()  # the lower threshold keeps more
+    chunked_prefill_column_dense_attention_forward(*args, threshold=0.08, **kw)
+    assert np.array_equal(calls[1][0].cpu().numpy()[Hkv:], table[Hkv:])
+    with pytest.raises(ValueError, match="threshold tensor has 3 values"):
+        chunked_prefill_column_dense_attention_forward(*args, threshold=torch.tensor([0.1, 0.2, 0.3]), **kw)
+    with pytest.raises(ValueError, match="Expected scalar or 1D"):
+        chunked_prefill_column_dense_attention_forward(*args, threshold=torch.ones((2, 1)), **kw)
+
+
+def test_seer_entry_short_gate_scores(gpu, monkeypatch):
+    """Gate scores over only the last key blocks (the reference right-aligns such a short keep
+    mask, _project_short_qhead_keep_block_to_kv_full_width, :708-734): the leading columns are
+    never selected, the covered ones follow the rule."""
+    _print_case(test="seer_entry_short_gate")
+    Hq, Hkv, Lq, past = 4, 2, 128, 64 * 20
+    ch = make_chunk([past], Lq, Hq, Hkv, seed=43)
+    P, cap = ch.past_blocks, ch.kv_cap
+    short = 12
+    g = torch.Generator().manual_seed(44)
+    gate_short = torch.rand((1, Hq, Lq // 64, short), generator=g) * 0.1
+    calls = spy_union_compact(monkeypatch)
+    chunked_prefill_column_dense_attention_forward(
+        ch.q.to(gpu), _seq_first(ch.k).to(gpu), _seq_first(ch.v).to(gpu), None, Lq, softmax_scale=SCALE,
+        attn_gate_score=gate_short.to(gpu), threshold=0.06, keep_recent_blocks=5, num_key_value_groups=Hq // Hkv)
+    full = torch.zeros((1, Hq, Lq // 64, cap))
+    full[..., cap - short:] = gate_short
+    ref_table, ref_counts = ref_seer_tables(full.numpy(), P, Hkv, 0.06, 5)
+    table, counts = (t.cpu().numpy() for t in calls[0])
+    assert np.array_equal(counts, ref_counts) and np.array_equal(table, ref_table)
+    assert all(ref_table[r, 0] >= cap - short for r in range(Hkv))
 
 
 def test_from_keep_block_matches_union(gpu):
@@ -285,3 +376,34 @@ def test_paged_cache_appends(gpu):
     nb = allk.shape[1] // 64
     assert float_bits_equal(f32(cache.kmean[:, :, :nb]), means)
     assert float_bits_equal(f32(cache.kgate[:, :, :nb]), oracle.gate_project(means, f32(wk), f32(cos), f32(sin), [0]))
+
+
+def test_paged_cache_summaries_after_decode_steps(gpu):
+    """Decode appends complete a block without summaries; the next chunk append recomputes its
+    mean-K from the cached keys, so every kmean equals a fresh computation over the whole
+    sequence (a stale or zero summary would differ); gate-K cannot be recomputed (the cache
+    has no pre-RoPE keys), so a gate append after such a block raises.  reset(keep_pages=True)
+    starts the counts again and the next sequence's summaries are its own."""
+    _print_case(test="paged_cache_summaries_after_decode")
+    Hkv = 2
+    g = torch.Generator().manual_seed(13)
+    wk = (torch.randn((Hkv, 128, 128), generator=g) * 0.02).float().to(gpu)
+    cos, sin = rope_tables(20)
+    cos, sin = cos.to(gpu), sin.to(gpu)
+    cache = PagedKVCache(1, Hkv, 64 * 12, gpu, with_kmean=True, with_kgate=True)
+    for seq in range(2):
+        parts = [torch.randn((1, n, Hkv, 128), generator=g).to(torch.bfloat16) for n in (320, 37, 27, 128)]
+        cache.append(parts[0].to(gpu), parts[0].to(gpu), gate_wk=wk, rope_cos=cos, rope_sin=sin)
+        cache.append_tokens(parts[1].to(gpu), parts[1].to(gpu))
+        cache.append_tokens(parts[2].to(gpu), parts[2].to(gpu))
+        assert (cache.length, cache.kmean_blocks, cache.kgate_blocks) == (384, 5, 5)
+        with pytest.raises(ValueError, match="gate-K summaries are missing"):
+            cache.append(parts[3].to(gpu), parts[3].to(gpu), gate_wk=wk, rope_cos=cos, rope_sin=sin)
+        assert cache.length == 384
+        cache.append(parts[3].to(gpu), parts[3].to(gpu))
+        assert (cache.length, cache.kmean_blocks) == (512, 8)
+        allk = torch.cat(parts, dim=1)
+        assert torch.equal(cache.k_hf().cpu(), allk.transpose(1, 2))
+        assert float_bits_equal(f32(cache.kmean[:, :, :8]), oracle.block_mean(bits(allk)))
+        cache.reset(keep_pages=True)
+        assert (cache.length, cache.kmean_blocks, cache.kgate_blocks) == (0, 0, 0)

@@ -22,8 +22,9 @@ from compactattention_amd.chunked_prefill import run_chunked_prefill_once, synth
 from compactattention_amd.prefill_sparse.llama import (SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaConfig,
                                                        SeerAttnLlamaFlashPrefillCompactAttnForCausalLM)
 from compactattention_amd.prefill_sparse.llama.modeling_llama_common import apply_rotary_pos_emb, project_qkv
+from compactattention_amd.synthetic import BASELINE_SEER
 
-from .util import bits, f32, oracle_gate_summaries
+from .util import bits, f32, oracle_gate_summaries, ref_seer_tables
 
 pytestmark = pytest.mark.gpu
 
@@ -32,7 +33,7 @@ T, CHUNK = 1280, 256
 
 def tiny_config(**kw) -> SeerAttnLlamaConfig:
     base = dict(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
-                num_key_value_heads=2, max_position_embeddings=2048, seerattn_threshold=0.02,
+                num_key_value_heads=2, max_position_embeddings=2048, seerattn_compactattn_threshold=0.02,
                 seerattn_flashprefill_alpha=0.3)
     base.update(kw)
     return SeerAttnLlamaConfig(**base)
@@ -103,7 +104,7 @@ def test_seer_keep_all_equals_dense(gpu):
     print("case: model keep-all vs dense", flush=True)
     ids = synthetic_prompt(1, T, 512, 99, gpu)
     dense = _model(SeerAttnLlamaChunkedDenseForCausalLM, gpu, seerattn_chunked_prefill_force_dense=True)
-    keep_all = _model(SeerAttnLlamaChunkedDenseForCausalLM, gpu, seerattn_threshold=-1.0)
+    keep_all = _model(SeerAttnLlamaChunkedDenseForCausalLM, gpu, seerattn_compactattn_threshold=-1.0)
     a, _ = run_chunked_prefill_once(dense, ids, CHUNK)
     b, _ = run_chunked_prefill_once(keep_all, ids, CHUNK)
     assert torch.equal(a, b)
@@ -140,7 +141,7 @@ def test_paged_cache_growth_matches_reserved_cache(gpu, cls):
     the same logits bit for bit as one into a cache reserved for the whole prompt, and the
     page tables are not the identity."""
     print(f"case: model cache growth {cls.__name__}", flush=True)
-    m = _model(cls, gpu, qk_scale=8.0, gate_scale=20.0, seerattn_threshold=0.1)
+    m = _model(cls, gpu, qk_scale=8.0, gate_scale=20.0, seerattn_compactattn_threshold=0.1)
     ids = synthetic_prompt(1, T, m.config.vocab_size, 5150, gpu)
     big = m.new_cache(1, T)
     small = m.new_cache(1, 128)
@@ -176,7 +177,7 @@ def test_unaligned_prompt_matches_fp32_reference(gpu, cls):
         assert cos > 0.999, (upto, cos)
         assert (got - ref).abs().max().item() <= 0.05 * ref.abs().max().item()
     if cls is SeerAttnLlamaChunkedDenseForCausalLM:
-        keep_all = _model(cls, gpu, seerattn_threshold=-1.0)
+        keep_all = _model(cls, gpu, seerattn_compactattn_threshold=-1.0)
         b, _ = run_chunked_prefill_once(keep_all, ids[:, :n], CHUNK)
         assert torch.equal(logits, b)
 
@@ -247,21 +248,30 @@ def _layer_qkv(attn, hidden, start, model):
 
 
 SEER_GATES = {
-    "seer": {},  # BASELINE config 1's gate: Qavg_Kavg, both sides projected per head
-    # the reference's default gate: no query projection, W_k [Hq, 384, 128] on max/min/avg K
-    "seer_default_gate": dict(seerattn_gate_type="Qavg_Kmaxminavg", seerattn_gate_force_double=False),
-    "seer_kv_aware_gate": dict(seerattn_gate_type="Qavg_Kmaxminavg", seerattn_gate_force_double=False,
-                               seerattn_compactattn_kv_group_aware_gate=True),
+    # the reference's default gate (no query projection, W_k [Hq, 384, 128] on max/min/avg K) and
+    # the reference's rule: threshold + the last keep_recent_blocks KV blocks
+    "seer": {},
+    # keep_recent_blocks beyond the chunk's 4 blocks: the 3 past blocks before it are forced
+    "seer_keep_recent_7": dict(seerattn_compactattn_keep_recent_blocks=7),
+    "seer_kv_aware_gate": dict(seerattn_compactattn_kv_group_aware_gate=True),
+    # BASELINE configs 1 and 3: Qavg_Kavg with force_double, threshold + sink + 2 local blocks
+    "seer_baseline": dict(BASELINE_SEER, seerattn_compactattn_threshold=0.1),
 }
 
 
-@pytest.mark.parametrize("selector", ["seer", "seer_default_gate", "seer_kv_aware_gate", "flashprefill"])
+@pytest.mark.parametrize("selector", ["seer", "seer_keep_recent_7", "seer_kv_aware_gate", "seer_baseline",
+                                      "flashprefill"])
 def test_layer_tables_bit_exact(gpu, selector):
+    """Per layer, the tables the model builds for its last chunk equal the reference's
+    selection recomputed from the layer's own inputs: for the Seer layer the restatement of the
+    reference's rule (tests/util.ref_seer_tables) on the oracle's gate scores; for BASELINE's
+    sink + local variant and FlashPrefill the oracle's rule."""
     print(f"case: model layer tables {selector}", flush=True)
     seer = selector.startswith("seer")
     cls = SeerAttnLlamaChunkedDenseForCausalLM if seer else SeerAttnLlamaFlashPrefillCompactAttnForCausalLM
-    m = _model(cls, gpu, qk_scale=8.0 if seer else 40.0, gate_scale=20.0, seerattn_threshold=0.1,
-               **SEER_GATES.get(selector, {}))
+    kw = dict(seerattn_compactattn_threshold=0.1)
+    kw.update(SEER_GATES.get(selector, {}))
+    m = _model(cls, gpu, qk_scale=8.0 if seer else 40.0, gate_scale=20.0, **kw)
     layer_idx = 1
     captured, handle, attn = _capture_layer_inputs(m, layer_idx)
     ids = synthetic_prompt(1, T, m.config.vocab_size, 7, gpu)
@@ -279,13 +289,17 @@ def test_layer_tables_bit_exact(gpu, selector):
     P = [stats["past_blocks"]]
     Hkv = m.config.num_key_value_heads
     c = m.config
+    table = counts = None
     if seer:
         bcos, bsin = (f32(t) for t in m.model.rotary_emb.blocks())
         qhat, khat = oracle_gate_summaries(attn.attn_gate, bits(q_nope), bits(k_nope_all), bcos, bsin, P[0])
         scores = oracle.block_scores(qhat, khat, P, 128 ** -0.5)
-        rule = oracle.Rule(threshold=c.seerattn_threshold, sink_blocks=c.compactattn_sink_blocks,
-                           local_blocks=c.compactattn_local_blocks)
-        last_n = 0
+        if selector == "seer_baseline":
+            rule = oracle.Rule(threshold=0.1, sink_blocks=1, local_blocks=2)
+            last_n = 0
+        else:
+            table, counts = ref_seer_tables(scores, P, Hkv, 0.1, c.seerattn_compactattn_keep_recent_blocks,
+                                            kv_group_aware=c.seerattn_compactattn_kv_group_aware_gate)
     else:
         qhat = oracle.block_mean(bits(q_rope))
         khat = oracle.block_mean(bits(k_rope_all))
@@ -295,14 +309,18 @@ def test_layer_tables_bit_exact(gpu, selector):
                            window_blocks=c.seerattn_flashprefill_window_size,
                            last_n_block=c.seerattn_flashprefill_last_n_block, topk_all_columns=True)
         last_n = c.seerattn_flashprefill_last_n_block
-    keep = oracle.select_rows(scores, P, rule)
-    _, _, table, counts = oracle.union_compact(keep, Hkv, P, last_n)
+    if table is None:
+        keep = oracle.select_rows(scores, P, rule)
+        _, _, table, counts = oracle.union_compact(keep, Hkv, P, last_n)
     got_counts = stats["counts"].cpu().numpy()
     got_table = stats["table"].cpu().numpy()
     assert np.array_equal(got_counts, counts)
-    assert np.array_equal(got_table, table)
+    assert np.array_equal(got_table[:, :table.shape[1]], table)
     nkb = P[0] + CHUNK // 64
     assert counts.min() < nkb, "the test wants a selective layer (some blocks dropped)"
+    if selector == "seer_keep_recent_7":
+        for r in range(Hkv):
+            assert {P[0] - 3, P[0] - 2, P[0] - 1} <= set(table[r, :counts[r]].tolist())
     # attention over the selected pages, recomputed from the layer's own inputs
     kc = k_rope_all.transpose(1, 2).contiguous()
     vc = v_all.transpose(1, 2).contiguous()
@@ -313,3 +331,90 @@ def test_layer_tables_bit_exact(gpu, selector):
                  128 ** -0.5, kc.shape[2] // 64, Hkv, out=out)
     err = np.abs(f32(out) - ref)
     assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
+
+
+def _seer_last_chunk_scores(attn, captured, block_rope, project):
+    """The oracle's gate scores of a Seer layer's last chunk, recomputed from the hidden states
+    the layer received (``captured``, one per chunk) through its own q/k projections."""
+    parts = [project(attn, h) for h in captured]
+    q_nope = parts[-1][0]
+    k_nope_all = torch.cat([p[1] for p in parts], dim=1)
+    P = [(k_nope_all.shape[1] - q_nope.shape[1]) // 64]
+    bcos, bsin = (f32(t) for t in block_rope)
+    qhat, khat = oracle_gate_summaries(attn.attn_gate, bits(q_nope), bits(k_nope_all), bcos, bsin, P[0])
+    return oracle.block_scores(qhat, khat, P, 128 ** -0.5), P
+
+
+def test_threshold_schedule_bands(gpu):
+    """seerattn_compactattn_threshold_schedule: the layer looks its threshold up by the chunk's
+    kv length (modeling_llama_seerattn_chunked_dense.py:36-98,225-227,871): a chunk ending at
+    1024 tokens takes the <= 1024 band's threshold, one ending at 1280 the <= 4096 band's; the
+    tables equal the reference's rule at that threshold and differ between the bands."""
+    print("case: model threshold schedule", flush=True)
+    sched = {"entries": [{"max_kv_len": 4096, "threshold": 0.3}, {"max_kv_len": 1024, "threshold": 0.02}]}
+    m = _model(SeerAttnLlamaChunkedDenseForCausalLM, gpu, qk_scale=8.0, gate_scale=20.0,
+               seerattn_compactattn_threshold=0.9, seerattn_compactattn_threshold_schedule=sched)
+    ids = synthetic_prompt(1, T, m.config.vocab_size, 7, gpu)
+    Hkv = m.config.num_key_value_heads
+    results = []
+    for upto, thr in ((1024, 0.02), (1280, 0.3)):
+        captured, handle, attn = _capture_layer_inputs(m, 1)
+        with torch.no_grad():
+            run_chunked_prefill_once(m, ids[:, :upto], CHUNK)
+        handle.remove()
+        with torch.no_grad():
+            scores, P = _seer_last_chunk_scores(attn, captured, m.model.rotary_emb.blocks(),
+                                                lambda a, h: project_qkv(a, h)[:2])
+        table, counts = ref_seer_tables(scores, P, Hkv, thr, 2)
+        stats = attn._compactattn_last_stats
+        assert np.array_equal(stats["counts"].cpu().numpy(), counts), upto
+        assert np.array_equal(stats["table"].cpu().numpy()[:, :table.shape[1]], table), upto
+        other, _ = ref_seer_tables(scores, P, Hkv, 0.3 if thr == 0.02 else 0.02, 2)
+        assert not np.array_equal(other, table), "the two bands should select differently"
+        results.append(counts)
+
+
+def test_hf_replacement_layer_tables_reference_rule(gpu):
+    """The stock-transformers replacement (seer_compactattn, the reference's default gate, no
+    sink or local blocks, keep_recent_blocks 2 and 6): the tables of a layer's last chunk equal
+    the reference's rule recomputed from the layer's inputs."""
+    transformers = pytest.importorskip("transformers")
+    from compactattention_amd.load_attention_replacement import (load_llama_attention_replacement_model,
+                                                                 new_compactattn_cache)
+
+    cfg = transformers.LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                                   num_attention_heads=4, num_key_value_heads=2, head_dim=128,
+                                   max_position_embeddings=2048)
+    for keep_recent in (2, 6):
+        print(f"case: hf replacement tables keep_recent={keep_recent}", flush=True)
+        torch.manual_seed(12)
+        stock = transformers.LlamaForCausalLM(cfg).eval()
+        with torch.no_grad():
+            for layer in stock.model.layers:
+                layer.self_attn.q_proj.weight.mul_(40.0)
+                layer.self_attn.k_proj.weight.mul_(40.0)
+        model = load_llama_attention_replacement_model(base_model=stock.to(gpu), variant="seer_compactattn",
+                                                       threshold=0.05, compactattn_keep_recent_blocks=keep_recent)
+        attn = model.model.layers[1].self_attn
+        c = model.compactattn_config
+        assert (c.compactattn_sink_blocks, c.compactattn_local_blocks) == (0, 0)
+        assert c.seerattn_gate_type == "Qavg_Kmaxminavg" and not c.seerattn_gate_force_double
+        with torch.no_grad():
+            attn.attn_gate.mask_linear_k.weight.mul_(20.0)
+        captured = []
+        handle = attn.register_forward_pre_hook(
+            lambda mod, args, kwargs: captured.append(kwargs["hidden_states"].detach().clone()), with_kwargs=True)
+        attn.compactattn_debug = True
+        ids = synthetic_prompt(1, T, cfg.vocab_size, 8, gpu)
+        cache = new_compactattn_cache(model, 1, T)
+        with torch.no_grad():
+            run_chunked_prefill_once(model, ids, CHUNK, cache)
+            handle.remove()
+            scores, P = _seer_last_chunk_scores(attn, captured, model.compactattn_block_rope.get(gpu),
+                                                lambda a, h: project_qkv(a, h)[:2])
+        table, counts = ref_seer_tables(scores, P, c.num_key_value_heads, 0.05, keep_recent)
+        stats = attn._compactattn_last_stats
+        assert stats["path"] == "chunked_selected"
+        assert np.array_equal(stats["counts"].cpu().numpy(), counts)
+        assert np.array_equal(stats["table"].cpu().numpy()[:, :table.shape[1]], table)
+        assert counts.min() < P[0] + CHUNK // 64, "the test wants a selective layer"

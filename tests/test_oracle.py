@@ -11,11 +11,12 @@ from __future__ import annotations
 import math
 
 import numpy as np
+import pytest
 import torch
 
 import oracle
 
-from .util import ref_flashprefill_rowwise, ref_flashprefill_tables
+from .util import ref_flashprefill_rowwise, ref_flashprefill_tables, ref_seer_tables
 
 RNG = np.random.default_rng(1234)
 
@@ -231,6 +232,47 @@ def test_select_local_blocks():
     got = oracle.select_rows(s, [10], oracle.Rule(local_blocks=2, sink_blocks=1))
     for q in range(2):
         assert set(np.nonzero(got[0, 0, q])[0].tolist()) == {0, 8, 9}
+
+
+def _gate_like_scores(rng, B, H, Qb, cap, past):
+    """Causal softmax rows (finite, summing to 1 over kb <= P + qb); the non-causal entries hold
+    1.0 so that a rule reading them would keep them."""
+    s = np.ones((B, H, Qb, cap), np.float32)
+    for b in range(B):
+        for q in range(Qb):
+            n = past[b] + q + 1
+            x = rng.standard_normal((H, n)) * 2.0
+            e = np.exp(x - x.max(-1, keepdims=True))
+            s[b, :, q, :n] = e / e.sum(-1, keepdims=True)
+    return s
+
+
+@pytest.mark.parametrize("Qb", [1, 3, 16])
+@pytest.mark.parametrize("kv_group_aware", [False, True])
+def test_seer_reference_rule_is_threshold_plus_local_blocks(Qb, kv_group_aware):
+    """The reference's Seer selection (fast path + KV-head union, restated in torch in
+    tests/util.ref_seer_tables) equals the oracle's strict threshold rule with local_blocks =
+    max(0, keep_recent_blocks - Qb), Q-block union and GQA union: the mapping the operator entry
+    and the Seer layer use.  Per-request thresholds select each request with its own value."""
+    rng = np.random.default_rng(100 + Qb)
+    Hkv, G = 2, 3
+    past = [37, 90]
+    cap = max(past) + Qb + 3
+    H = Hkv if kv_group_aware else Hkv * G
+    s = _gate_like_scores(rng, 2, H, Qb, cap, past)
+    for keep_recent in (0, 1, 2, 4, Qb + 5, 200):
+        for thr in (0.05, [0.02, 0.1]):
+            ref_t, ref_c = ref_seer_tables(s, past, Hkv, thr, keep_recent, kv_group_aware=kv_group_aware)
+            local = max(0, keep_recent - Qb)
+            thrs = thr if isinstance(thr, list) else [thr, thr]
+            keep = np.concatenate([oracle.select_rows(s[b:b + 1], past[b:b + 1],
+                                                      oracle.Rule(threshold=thrs[b], local_blocks=local))
+                                   for b in range(2)])
+            _, _, t, c = oracle.union_compact(keep, Hkv, past)
+            assert np.array_equal(c, ref_c), (keep_recent, thr)
+            assert np.array_equal(t[:, :ref_t.shape[1]], ref_t), (keep_recent, thr)
+            if keep_recent <= Qb + 1:
+                assert (ref_c < np.repeat(np.array(past) + Qb, Hkv)).any(), "the case should drop blocks"
 
 
 def test_union_compact_matches_reference_csr_spec():

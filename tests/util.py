@@ -170,3 +170,58 @@ def torch_reference_check(out, q, k_hf, v_hf, past_blocks, table, counts, scale,
     assert worst <= atol_max and mean <= atol_mean, (worst, mean)
     assert lse_worst <= lse_atol, lse_worst
     return worst, mean
+
+
+def ref_seer_tables(scores, past, Hkv, threshold, keep_recent_blocks, kv_group_aware=False):
+    """Restatement of the reference's Seer selection for a chunk: _build_keep_block_mask_chunked_
+    fast_path (compact_attn/modules/attention_forward_chunked_dense.py:559-638) -- past column kb
+    kept iff the max over the query blocks of score[qb, kb] > threshold, current column j iff the
+    max over the query blocks that see it (qb >= j, the suffix max at the diagonal) > threshold,
+    then the last keep_recent_blocks of the Kb = P + Qb columns set -- and
+    _build_kv_head_union_keep_block_mask (:641-683): the past columns OR-ed over the G heads of
+    a KV group (a kv-group-aware gate's rows are the KV groups already), the current chunk open
+    (and the preprojected path's current-open step, :1044-1050).  threshold is a float or a
+    sequence with one value per request.  scores [B, Hs, Qb, >= P+Qb]; returns (table [B*Hkv,
+    cap] -1 padded with cap = scores.shape[-1], counts)."""
+    s_all = torch.as_tensor(np.asarray(scores), dtype=torch.float32)
+    B, Hs, Qb, cap = s_all.shape
+    G = 1 if kv_group_aware else Hs // Hkv
+    thr = list(threshold) if isinstance(threshold, (list, tuple, np.ndarray)) else [float(threshold)] * B
+    table = np.full((B * Hkv, cap), -1, np.int32)
+    counts = np.zeros((B * Hkv,), np.int32)
+    for b in range(B):
+        P = int(past[b])
+        Kb = P + Qb
+        s = s_all[b, :, :, :Kb]
+        keep_past = s[..., :P].amax(dim=1) > thr[b]
+        curr = s[..., P:Kb]  # [H, Qb, Qb]
+        suffix = torch.flip(torch.cummax(torch.flip(curr, dims=[1]), dim=1).values, dims=[1])
+        j = torch.arange(Qb)
+        keep_curr = suffix[:, j, j] > thr[b]
+        keep = torch.cat([keep_past, keep_curr], dim=-1)
+        recent = min(int(keep_recent_blocks), Kb)
+        if recent > 0:
+            keep[:, Kb - recent:] = True
+        kv_past = keep[:, :P].view(Hkv, G, P).any(dim=1)
+        kv = torch.cat([kv_past, torch.ones((Hkv, Qb), dtype=torch.bool)], dim=-1)
+        for hk in range(Hkv):
+            ids = torch.nonzero(kv[hk]).flatten().numpy()
+            table[b * Hkv + hk, :len(ids)] = ids
+            counts[b * Hkv + hk] = len(ids)
+    return table, counts
+
+
+def spy_union_compact(monkeypatch):
+    """Records the (table, counts) of every ops.union_compact call the code under test makes."""
+    from compactattention_amd import ops
+
+    calls = []
+    real = ops.union_compact
+
+    def spy(*args, **kw):
+        out = real(*args, **kw)
+        calls.append((out[0].detach().clone(), out[1].detach().clone()))
+        return out
+
+    monkeypatch.setattr(ops, "union_compact", spy)
+    return calls
