@@ -713,7 +713,8 @@ def model_prefill(tokens, chunk, layers, dev, seer_only: bool = False):
     torch.cuda.empty_cache()
 
     fcfg = SeerAttnLlamaConfig(num_hidden_layers=layers, max_position_embeddings=max(tokens, 131072),
-                               seerattn_flashprefill_alpha=1.0, seerattn_flashprefill_attention_sink=2,
+                               seerattn_flashprefill_block_size=64, seerattn_flashprefill_alpha=1.0,
+                               seerattn_flashprefill_attention_sink=2,
                                seerattn_flashprefill_window_size=4, seerattn_flashprefill_last_n_block=0)
     fmodel = SeerAttnLlamaFlashPrefillCompactAttnForCausalLM(fcfg, device=dev)
     fmodel.load_state_dict(state, strict=False)  # the same decoder weights
@@ -774,7 +775,8 @@ def module_attention(dev, past: int = 131072, chunk: int = 1024, keep: float = 0
         LlamaFlashPrefillCompactAttnAttention
 
     cfg = SeerAttnLlamaConfig(num_hidden_layers=1, max_position_embeddings=past + chunk,
-                              seerattn_flashprefill_alpha=1.0, seerattn_flashprefill_attention_sink=2,
+                              seerattn_flashprefill_block_size=64, seerattn_flashprefill_alpha=1.0,
+                              seerattn_flashprefill_attention_sink=2,
                               seerattn_flashprefill_window_size=4, seerattn_flashprefill_last_n_block=0)
     g = torch.Generator(device=dev)
     g.manual_seed(1234)

@@ -44,6 +44,7 @@ EXPORTED = (
     "ca_cache_fill_pool_query",
     "ca_gate_key_summaries",
     "ca_gate_query_summaries",
+    "ca_pair_block_summaries",
     "ca_score_select",
     "ca_select_scores",
     "ca_union_compact",
@@ -133,6 +134,7 @@ _SIGNATURES = {
                                              _vp]),
     "ca_gate_query_summaries": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _i32, _vp, _i32, _vp, _vp, _i64,
                                                _vp, _vp]),
+    "ca_pair_block_summaries": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp]),
     "ca_score_select": (ctypes.c_int, [_P(Dims), _vp, _vp, _f32, _P(SelectRule), _vp, _vp, _vp, _vp]),
     "ca_select_scores": (ctypes.c_int, [_P(Dims), _vp, _i32, _i64, _i64, _i64, _P(SelectRule), _vp, _vp, _vp]),
     "ca_union_compact": (ctypes.c_int, [_P(Dims), _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),

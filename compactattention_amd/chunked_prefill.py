@@ -22,8 +22,8 @@ def run_chunked_prefill_once(model: torch.nn.Module, input_ids: torch.Tensor, ch
     B, T = input_ids.shape
     if chunk_size <= 0 or chunk_size % 64:
         raise ValueError("chunk_size must be a positive multiple of 64")
-    # a prompt of any length: a final chunk that is not a multiple of 64 tokens selects over
-    # its whole blocks and runs its last T % 64 tokens as one dense step (split_unaligned_chunk)
+    # a prompt of any length: a final chunk that is not a multiple of 64 tokens selects with a
+    # partial last block
     # a stock transformers model whose attention was replaced (load_attention_replacement)
     # takes the cache as past_key_values and returns a model output
     hf = getattr(getattr(model, "config", None), "seerattn_attention_harness", None) == "replacement"

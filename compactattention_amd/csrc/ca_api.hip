@@ -49,19 +49,19 @@ int check_dims(const ca_dims* d, const int32_t* past_host, ca::Shape* s, ca::Pas
     if (d->batch < 1 || d->batch > CA_MAX_BATCH)
         return fail(d->batch < 1 ? CA_ERR_INVALID : CA_ERR_LIMIT, "batch=%d outside [1, %d]",
                     d->batch, CA_MAX_BATCH);
-    if (d->q_len <= 0 || d->q_len % CA_BLOCK != 0)
-        return fail(CA_ERR_INVALID, "q_len=%d must be a positive multiple of %d", d->q_len, CA_BLOCK);
+    if (d->q_len <= 0) return fail(CA_ERR_INVALID, "q_len=%d must be positive", d->q_len);
     if (d->num_q_heads <= 0 || d->num_kv_heads <= 0 || d->num_q_heads % d->num_kv_heads != 0)
         return fail(CA_ERR_INVALID, "num_q_heads=%d must be a positive multiple of num_kv_heads=%d",
                     d->num_q_heads, d->num_kv_heads);
     const int G = d->num_q_heads / d->num_kv_heads;
     if (G > 16) return fail(CA_ERR_LIMIT, "GQA group size %d > 16", G);
-    const int Qb = d->q_len / CA_BLOCK;
+    // the chunk's blocks: the last one holds q_len % 64 tokens when q_len is not a multiple of 64
+    const int Qb = (d->q_len + CA_BLOCK - 1) / CA_BLOCK;
     int mx = 0;
     for (int b = 0; b < d->batch; ++b) {
         if (past_host[b] < 0) return fail(CA_ERR_INVALID, "past_blocks[%d]=%d < 0", b, past_host[b]);
         if ((int64_t)past_host[b] + Qb > d->kv_cap)
-            return fail(CA_ERR_INVALID, "past_blocks[%d]=%d + q_len/64=%d exceeds kv_cap=%d", b,
+            return fail(CA_ERR_INVALID, "past_blocks[%d]=%d + ceil(q_len/64)=%d exceeds kv_cap=%d", b,
                         past_host[b], Qb, d->kv_cap);
         pb->p[b] = past_host[b];
         if (past_host[b] + Qb > mx) mx = past_host[b] + Qb;
@@ -359,6 +359,25 @@ int ca_pool_query(const ca_dims* dims, const ca_seq_layout* q, const int32_t* pa
                                          gate_wq ? rope_sin : nullptr, qhat, CA_POOL_AVG, false,
                                          static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "pool_query launch");
+    return ok();
+}
+
+int ca_pair_block_summaries(const float* src, int64_t src_stride, float* dst, int64_t dst_stride, int64_t rows,
+                            int32_t n_blocks, int32_t last_tokens, void* stream) {
+    if (src == nullptr || dst == nullptr) return fail(CA_ERR_INVALID, "src and dst are required");
+    if (!aligned16(src) || !aligned16(dst)) return fail(CA_ERR_INVALID, "src and dst must be 16-byte aligned");
+    if (rows < 1 || n_blocks < 1) return fail(CA_ERR_INVALID, "rows=%lld and n_blocks=%d must be positive",
+                                              (long long)rows, n_blocks);
+    if (last_tokens < 1 || last_tokens > CA_BLOCK)
+        return fail(CA_ERR_INVALID, "last_tokens=%d outside [1, %d]", last_tokens, CA_BLOCK);
+    const int npairs = (n_blocks + 1) / 2;
+    if (src_stride < n_blocks || dst_stride < npairs)
+        return fail(CA_ERR_INVALID, "row strides (%lld, %lld blocks) below (%d, %d)", (long long)src_stride,
+                    (long long)dst_stride, n_blocks, npairs);
+    if (rows * npairs > ((int64_t)1 << 36)) return fail(CA_ERR_LIMIT, "too many rows");
+    hipError_t e = ca::launch_pair_summaries(src, src_stride, dst, dst_stride, rows, n_blocks, last_tokens,
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "pair_summaries launch");
     return ok();
 }
 

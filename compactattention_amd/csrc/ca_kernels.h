@@ -56,6 +56,11 @@ hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks&
 // LDS bytes the score/select kernel needs for this shape (0 if unsupported).
 size_t score_select_lds_bytes(const Shape& s, bool compute);
 
+// 128-token block summaries from pairs of 64-token ones (rows of n_blocks source blocks, the last
+// holding last_tokens tokens)
+hipError_t launch_pair_summaries(const float* src, int64_t src_stride, float* dst, int64_t dst_stride,
+                                 int64_t rows, int n_blocks, int last_tokens, hipStream_t stream);
+
 hipError_t launch_score_select(const Shape& s, const float* qhat, const float* khat, float scale,
                                const void* scores_in, int dtype, int64_t ssb, int64_t ssh,
                                int64_t ssq, const ca_select_rule& rule, const PastBlocks& pb,

@@ -64,24 +64,30 @@ __device__ void gate_project_rope(const float* xs, int in, const float* w, const
 // ---------------------------------------------------------------------------------------
 // Block staging shared by cache fill and query pooling: 256 threads move one 64-token x 128
 // block with 16-byte accesses (thread t: token t/16 + 16 i, 8-element chunk t%16) and keep
-// a bf16 copy in LDS; the block mean is then a sequential sum over the 64 tokens per head
-// dim (threads 0..127), times 1/64.
+// a bf16 copy in LDS; the block mean is then a sequential sum over the block's nv tokens per
+// head dim (threads 0..127), divided by nv.  A chunk's last block holds nv < 64 tokens when
+// its length is not a multiple of 64: only those rows are read, written and pooled.
 constexpr int kTilePitch = kD + 8;  // bf16 elements per staged token row
 
-__device__ __forceinline__ float block_mean_from_lds(const uint16_t* tile, int d) {
-    float sum = 0.0f;
-#pragma unroll 16
-    for (int t = 0; t < kBlock; ++t) sum = sum + bf16_to_f32(tile[t * kTilePitch + d]);
-    return sum * 0.015625f;
+// tokens of block j of a chunk of q_len tokens
+__device__ __forceinline__ int block_tokens(int q_len, int j) {
+    return min(kBlock, q_len - j * kBlock);
 }
 
-// AttnGate pooling of head dim d over the 64 staged tokens (attn_gate.py:113-130,233-237):
+__device__ __forceinline__ float block_mean_from_lds(const uint16_t* tile, int d, int nv) {
+    float sum = 0.0f;
+#pragma unroll 16
+    for (int t = 0; t < nv; ++t) sum = sum + bf16_to_f32(tile[t * kTilePitch + d]);
+    return sum / static_cast<float>(nv);  // = sum * (1/64) bit for bit when nv = 64
+}
+
+// AttnGate pooling of head dim d over the nv staged tokens (attn_gate.py:113-130,233-237):
 // the selected pools in the order max, min, avg go to xs[c*128 + d], c = 0, 1, ...  max and
 // min are strict compares from token 0 (bf16 values, exact); avg is block_mean_from_lds.
-__device__ __forceinline__ void block_pool_from_lds(const uint16_t* tile, int d, int pools, float* xs) {
+__device__ __forceinline__ void block_pool_from_lds(const uint16_t* tile, int d, int pools, int nv, float* xs) {
     float mx = bf16_to_f32(tile[d]), mn = mx, sum = 0.0f;
 #pragma unroll 16
-    for (int t = 0; t < kBlock; ++t) {
+    for (int t = 0; t < nv; ++t) {
         const float v = bf16_to_f32(tile[t * kTilePitch + d]);
         mx = v > mx ? v : mx;
         mn = v < mn ? v : mn;
@@ -90,7 +96,7 @@ __device__ __forceinline__ void block_pool_from_lds(const uint16_t* tile, int d,
     int c = 0;
     if (pools & CA_POOL_MAX) xs[kD * c++ + d] = mx;
     if (pools & CA_POOL_MIN) xs[kD * c++ + d] = mn;
-    if (pools & CA_POOL_AVG) xs[kD * c++ + d] = sum * 0.015625f;
+    if (pools & CA_POOL_AVG) xs[kD * c++ + d] = sum / static_cast<float>(nv);
 }
 
 __device__ __forceinline__ int pool_count(int pools) {
@@ -109,13 +115,17 @@ __device__ __forceinline__ void cache_fill_block(const Shape& s, const SeqAddr& 
     const int b = row / s.Hkv;
     const int hk = row - b * s.Hkv;
     const int kb = pb.p[b] + j;
+    const int nv = block_tokens(s.Lq, j);
     const int t = threadIdx.x;
     const int tok0 = t >> 4;
     const int ch = t & 15;
     const uint16_t* ks = kn.data + b * kn.sb + (int64_t)j * kBlock * kn.st + hk * kn.sh + 8 * ch;
     u32x4_v kr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kr[i] = *reinterpret_cast<const u32x4_v*>(ks + (int64_t)(tok0 + 16 * i) * kn.st);
+    for (int i = 0; i < 4; ++i) {
+        const u32x4_v z = {0u, 0u, 0u, 0u};
+        kr[i] = tok0 + 16 * i < nv ? *reinterpret_cast<const u32x4_v*>(ks + (int64_t)(tok0 + 16 * i) * kn.st) : z;
+    }
     if (kc.data != nullptr) {  // append K and V (summaries-only calls pass no cache)
         const int64_t kphys = kc.page_table ? clamp_page(kc.page_table[(int64_t)row * kc.pts + kb], kc.max_page) : kb;
         const int64_t vphys = vc.page_table ? clamp_page(vc.page_table[(int64_t)row * vc.pts + kb], vc.max_page) : kb;
@@ -124,12 +134,17 @@ __device__ __forceinline__ void cache_fill_block(const Shape& s, const SeqAddr& 
         uint16_t* vd = vc.data + b * vc.sb + hk * vc.sh + vphys * vc.sblk + 8 * ch;
         u32x4_v vr[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) vr[i] = *reinterpret_cast<const u32x4_v*>(vsrc + (int64_t)(tok0 + 16 * i) * vn.st);
+        for (int i = 0; i < 4; ++i) {
+            const u32x4_v z = {0u, 0u, 0u, 0u};
+            vr[i] = tok0 + 16 * i < nv ? *reinterpret_cast<const u32x4_v*>(vsrc + (int64_t)(tok0 + 16 * i) * vn.st) : z;
+        }
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tok = tok0 + 16 * i;
-            *reinterpret_cast<u32x4_v*>(kd + (int64_t)tok * kc.stok) = kr[i];
-            *reinterpret_cast<u32x4_v*>(vd + (int64_t)tok * vc.stok) = vr[i];
+            if (tok < nv) {
+                *reinterpret_cast<u32x4_v*>(kd + (int64_t)tok * kc.stok) = kr[i];
+                *reinterpret_cast<u32x4_v*>(vd + (int64_t)tok * vc.stok) = vr[i];
+            }
         }
     }
 #pragma unroll
@@ -137,8 +152,8 @@ __device__ __forceinline__ void cache_fill_block(const Shape& s, const SeqAddr& 
     if (kmean == nullptr && wk == nullptr) return;
     __syncthreads();
     if (t < kD) {
-        if (kmean) kmean[((int64_t)row * s.cap + kb) * kD + t] = block_mean_from_lds(tile, t);
-        if (wk) block_pool_from_lds(tile, t, pools, xs);
+        if (kmean) kmean[((int64_t)row * s.cap + kb) * kD + t] = block_mean_from_lds(tile, t, nv);
+        if (wk) block_pool_from_lds(tile, t, pools, nv, xs);
     }
     if (wk == nullptr) return;
     __syncthreads();
@@ -189,6 +204,7 @@ __device__ __forceinline__ void pool_query_block(const Shape& s, const SeqAddr& 
     const int ch = t & 15;
     const int C = pool_count(pools);
     const int nsrc = kv_aware ? s.G : 1;
+    const int nv = block_tokens(s.Lq, qb);
     float* out = qhat + ((int64_t)bh * s.Qb + qb) * kD;
     for (int g = 0; g < nsrc; ++g) {
         const int hq = kv_aware ? h * s.G + g : h;
@@ -197,12 +213,13 @@ __device__ __forceinline__ void pool_query_block(const Shape& s, const SeqAddr& 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tok = tok0 + 16 * i;
-            *reinterpret_cast<u32x4_v*>(tile + tok * kTilePitch + 8 * ch) =
-                *reinterpret_cast<const u32x4_v*>(sp + (int64_t)tok * q.st);
+            if (tok < nv)
+                *reinterpret_cast<u32x4_v*>(tile + tok * kTilePitch + 8 * ch) =
+                    *reinterpret_cast<const u32x4_v*>(sp + (int64_t)tok * q.st);
         }
         __syncthreads();
         if (t < kD) {
-            block_pool_from_lds(tile, t, pools, xs + g * C * kD);
+            block_pool_from_lds(tile, t, pools, nv, xs + g * C * kD);
             if (wq == nullptr && rope_cos == nullptr) out[t] = xs[t];  // one pool, no projection, no RoPE
         }
     }
@@ -1174,6 +1191,38 @@ __global__ __launch_bounds__(kCsrThreads) void table_csr_kernel(CsrParams p) {
 }
 
 
+// 128-token block summaries from pairs of 64-token ones (FlashPrefill with 128-token score
+// blocks): dst[j] = (c0 * src[2j] + c1 * src[2j + 1]) / (c0 + c1) with the blocks' token counts
+// c (64, or last_tokens for the last source block) -- two products, one sum, one correctly
+// rounded division, in that order -- and dst[j] = src[2j] when block 2j has no partner.  One
+// thread per four head dims of one (row, pair).
+__global__ __launch_bounds__(256) void pair_summaries_kernel(const float* src, int64_t src_stride, float* dst,
+                                                             int64_t dst_stride, int64_t rows, int n_blocks,
+                                                             int last_tokens) {
+    const int npairs = (n_blocks + 1) / 2;
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (gid >= rows * npairs * 32) return;
+    const int q = static_cast<int>(gid & 31);
+    const int64_t rp = gid >> 5;
+    const int64_t row = rp / npairs;
+    const int j = static_cast<int>(rp - row * npairs);
+    const int b0 = 2 * j;
+    const float* s0 = src + (row * src_stride + b0) * kD + 4 * q;
+    float4 out = *reinterpret_cast<const float4*>(s0);
+    if (b0 + 1 < n_blocks) {
+        const float c0 = b0 == n_blocks - 1 ? static_cast<float>(last_tokens) : 64.0f;
+        const float c1 = b0 + 1 == n_blocks - 1 ? static_cast<float>(last_tokens) : 64.0f;
+        const float4 m1 = *reinterpret_cast<const float4*>(s0 + kD);
+        const float n = c0 + c1;
+        const float4 m0 = out;
+        out.x = (c0 * m0.x + c1 * m1.x) / n;
+        out.y = (c0 * m0.y + c1 * m1.y) / n;
+        out.z = (c0 * m0.z + c1 * m1.z) / n;
+        out.w = (c0 * m0.w + c1 * m1.w) / n;
+    }
+    *reinterpret_cast<float4*>(dst + (row * dst_stride + j) * kD + 4 * q) = out;
+}
+
 }  // namespace
 
 hipError_t launch_cache_fill(const Shape& s, const SeqAddr& k_new, const SeqAddr& v_new,
@@ -1203,6 +1252,14 @@ hipError_t launch_pool_query(const Shape& s, const SeqAddr& q, const PastBlocks&
     const size_t xs_bytes = sizeof(float) * kD * (kv_aware ? s.G : 1) * __builtin_popcount(pools & 7);
     hipLaunchKernelGGL(pool_query_kernel, grid, dim3(256), xs_bytes, stream, s, q, pb, wq, rope_cos,
                        rope_sin, qhat, pools, kv_aware ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_pair_summaries(const float* src, int64_t src_stride, float* dst, int64_t dst_stride,
+                                 int64_t rows, int n_blocks, int last_tokens, hipStream_t stream) {
+    const int64_t threads = rows * ((n_blocks + 1) / 2) * 32;
+    hipLaunchKernelGGL(pair_summaries_kernel, dim3(static_cast<unsigned>((threads + 255) / 256)), dim3(256), 0,
+                       stream, src, src_stride, dst, dst_stride, rows, n_blocks, last_tokens);
     return hipGetLastError();
 }
 

@@ -197,14 +197,17 @@ class PagedKVCache:
     # -- appends --------------------------------------------------------------------------
     def append(self, k_new: torch.Tensor, v_new: torch.Tensor, gate_wk: Optional[torch.Tensor] = None,
                rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None) -> int:
-        """Append [B, L, Hkv, 128] bf16 K/V (L a multiple of 64) through the cache-fill kernel,
-        which also writes the new blocks' kmean (and, with gate_wk [Hkv, 128, 128], the
-        avg-pooled gate-K summaries); returns the number of past blocks before the append."""
+        """Append a chunk of [B, L, Hkv, 128] bf16 K/V at a block boundary through the cache-fill
+        kernel, which also writes the new blocks' kmean (and, with gate_wk [Hkv, 128, 128], the
+        avg-pooled gate-K summaries); returns the number of past blocks before the append.  When
+        L is not a multiple of 64 the last block holds L % 64 tokens: its summaries pool those
+        (a kgate one stays valid, as the reference's gate cache keeps it; a kmean one is
+        recomputed once decode tokens complete the block)."""
         B, L, Hkv, _ = k_new.shape
         if B != self.batch or Hkv != self.num_kv_heads:
             raise ValueError("k_new does not match the cache's batch / KV heads")
-        if L % BLOCK:
-            raise ValueError("appended chunks must be multiples of 64 tokens")
+        if L < 1:
+            raise ValueError("appended chunks hold at least one token")
         if self.length % BLOCK:
             raise ValueError("chunked prefill cannot follow decode steps that left a partial block")
         if gate_wk is not None and (self.kgate is None or self.kgate_heads != Hkv):
@@ -213,7 +216,7 @@ class PagedKVCache:
         if gate_wk is not None:
             self.require_kgate(past)
         self.refresh_kmean(past)
-        self._map(past, past + L // BLOCK)
+        self._map(past, past - (-L // BLOCK))
         K, V = self.layouts()
         ops.cache_fill(k_new, v_new, K, V, [past] * B, self.cap, self.kmean, gate_wk=gate_wk, rope_cos=rope_cos,
                        rope_sin=rope_sin, kgate=self.kgate if gate_wk is not None else None)
@@ -221,26 +224,26 @@ class PagedKVCache:
         if self.kmean is not None:
             self.kmean_blocks = self.past_blocks
         if gate_wk is not None:
-            self.kgate_blocks = self.past_blocks
+            self.kgate_blocks = -(-self.length // BLOCK)
         return past
 
     def append_with_query_means(self, k_new: torch.Tensor, v_new: torch.Tensor,
                                 q: torch.Tensor) -> Tuple[int, torch.Tensor]:
         """append(k_new, v_new) and the chunk's query-block means ([B, L, Hq, 128] bf16 ->
-        qhat [B, Hq, L/64, 128] fp32, the FlashPrefill pooled queries) in one kernel launch;
+        qhat [B, Hq, ceil(L/64), 128] fp32, the FlashPrefill pooled queries) in one kernel launch;
         returns (past blocks before the append, qhat)."""
         B, L, Hkv, _ = k_new.shape
         if B != self.batch or Hkv != self.num_kv_heads:
             raise ValueError("k_new does not match the cache's batch / KV heads")
-        if L % BLOCK:
-            raise ValueError("appended chunks must be multiples of 64 tokens")
+        if L < 1:
+            raise ValueError("appended chunks hold at least one token")
         if self.length % BLOCK:
             raise ValueError("chunked prefill cannot follow decode steps that left a partial block")
         if self.kmean is None:
             raise ValueError("cache built without the mean-K summaries")
         past = self.past_blocks
         self.refresh_kmean(past)
-        self._map(past, past + L // BLOCK)
+        self._map(past, past - (-L // BLOCK))
         K, V = self.layouts()
         qhat = ops.cache_fill_pool_query(k_new, v_new, K, V, [past] * B, self.cap, self.kmean, q)
         self.length += L

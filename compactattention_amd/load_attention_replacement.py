@@ -10,7 +10,6 @@ by the reference's key names) and returns the transformers 2-tuple ``(attn_outpu
 Differences from the reference, each raised as ``ValueError`` rather than ignored:
 - only the compactattn variants (``seer_compactattn``, ``seer_compactattn_hf``,
   ``flashprefill_compactattn``) exist here; the block-sparse variants are outside this path;
-- FlashPrefill runs 64-token blocks (the reference defaults to 128);
 - ``base_model`` is a transformers ``LlamaForCausalLM`` instance or a local directory (there
   is no hub download), and gate weights load from a local ``attn_gate_weights.pth`` with
   ``torch.load(weights_only=True)``.
@@ -196,7 +195,7 @@ def load_llama_attention_replacement_model(
     threshold: float = 3e-4,
     compactattn_keep_recent_blocks: int = 2,
     flashprefill_alpha: float = 0.01,
-    flashprefill_block_size: int = 64,
+    flashprefill_block_size: int = 128,
     flashprefill_attention_sink: int = 2,
     flashprefill_window_size: int = 4,
     flashprefill_last_n_block: int = 2,

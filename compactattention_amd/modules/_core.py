@@ -43,6 +43,10 @@ class ChunkGeometry:
 
 
 def geometry(query_states: torch.Tensor, kv_len: int, num_kv_heads: int, block_size: int) -> ChunkGeometry:
+    """The chunk's block geometry.  The chunk starts at a block boundary (kv_len - q_len a
+    multiple of 64) and covers Qb = ceil(q_len / 64) blocks; when q_len is not a multiple of
+    64 its last block holds q_len % 64 tokens, which the kernels read, pool and attend up to
+    kv_len only (a partial block selects and is attended like a whole one)."""
     if block_size != BLOCK:
         raise ValueError(f"block_size={block_size}: this build runs 64-token blocks only")
     if query_states.dim() != 4 or query_states.shape[-1] != HEAD_DIM:
@@ -50,39 +54,34 @@ def geometry(query_states: torch.Tensor, kv_len: int, num_kv_heads: int, block_s
     bsz, q_len, num_q_heads, _ = query_states.shape
     if num_q_heads % num_kv_heads:
         raise ValueError(f"num_q_heads={num_q_heads} is not a multiple of num_kv_heads={num_kv_heads}")
-    if q_len % BLOCK or kv_len % BLOCK:
-        raise ValueError(f"q_len={q_len} and kv_len={kv_len} must be multiples of {BLOCK} (chunk boundaries "
-                         "are block aligned)")
-    if kv_len < q_len:
+    if kv_len < q_len or q_len < 1:
         raise ValueError(f"kv_len={kv_len} < q_len={q_len}")
+    if (kv_len - q_len) % BLOCK:
+        raise ValueError(f"a chunk of {q_len} queries over {kv_len} keys must start at a 64-token block boundary")
     P = (kv_len - q_len) // BLOCK
-    Qb = q_len // BLOCK
+    Qb = -(-q_len // BLOCK)
     return ChunkGeometry(bsz, q_len, kv_len, num_q_heads, num_kv_heads, P, Qb, P + Qb)
 
 
-def aligned_head(q_len: int, kv_len: int) -> Optional[int]:
-    """None for a block-aligned call (q_len and kv_len multiples of 64).  Otherwise the query
-    tokens of its block-aligned head: 0 when fewer than 64 queries (the whole call attends
-    densely), else q_len rounded down to 64 -- the head runs the selecting path over the first
-    kv_len - (q_len - head) keys and the last q_len % 64 queries attend densely to all kv_len
-    keys (dense_tail).  A chunk of 64 or more queries must start at a block boundary."""
-    if q_len % BLOCK == 0 and kv_len % BLOCK == 0:
-        return None
+def starts_mid_block(q_len: int, kv_len: int) -> bool:
+    """A chunk that does not start at a 64-token block boundary (decode tokens left the cache
+    between two blocks): its queries attend densely (dense_tail) when there are at most 64 of
+    them; a longer such chunk raises, as its first query block would straddle two key blocks."""
     if kv_len < q_len:
         raise ValueError(f"kv_len={kv_len} < q_len={q_len}")
-    if q_len < BLOCK:
-        return 0
-    if (kv_len - q_len) % BLOCK:
+    if (kv_len - q_len) % BLOCK == 0:
+        return False
+    if q_len > BLOCK:
         raise ValueError(f"a chunk of {q_len} queries over {kv_len} keys must start at a 64-token block boundary")
-    return q_len - q_len % BLOCK
+    return True
 
 
 def dense_tail(query_states: torch.Tensor, K: ops.KV, V: ops.KV, kv_len: int, num_kv_heads: int,
                softmax_scale: Optional[float]) -> torch.Tensor:
     """Queries [B, n, Hq, 128] (n <= 64) at the last n of kv_len positions attend to every key
     before them (bottom-right causal) through the decode kernel, which reads the partial last
-    block up to kv_len only -- the reference's dense fallback (flashprefill_prefill.py:903-907,
-    _dense_prefill_full_kv)."""
+    block up to kv_len only -- the reference's dense attention for q_len == 1
+    (modeling_llama_seerattn_chunked_dense.py:878-894, flashprefill_prefill.py:903-907)."""
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(HEAD_DIM)
     B = query_states.shape[0]
     return ops.attn_decode(query_states, K, V, [kv_len] * B, scale, -(-kv_len // BLOCK), num_kv_heads)

@@ -18,10 +18,14 @@ chunk's block count), the current chunk is always attended, and the KV group tak
 of its Q heads.  The threshold is a float or a tensor with one value per request (:383-393).
 
 Supported inputs (anything else raises ValueError): block_size 64, no padding in
-attention_mask, head_dim 128, bf16 Q/K/V on the GPU.  A call whose q_len or kv_len is not a
-multiple of 64 selects for its block-aligned head and attends densely for its last q_len % 64
-queries (all of them below 64 queries); such a chunk of 64 or more queries must start at a
-block boundary.
+attention_mask, head_dim 128, bf16 Q/K/V on the GPU.  A chunk whose length is not a multiple
+of 64 selects and attends through the same path, its last block holding q_len % 64 tokens:
+its queries see the selected past blocks and the current chunk causally, as the reference's
+padded indexed path intends (_maybe_pad_indexed_dense_tail_inputs, :438-491; that path
+aligns flash-attn's bottom-right causal mask to the padded key length, so each of its
+queries also sees the next 64 - q_len % 64 positions, future tokens or zero-padded keys --
+here the mask is at the true positions).  A chunk that starts inside a block (after decode
+steps) attends densely when it has at most 64 queries, and raises otherwise.
 """
 from __future__ import annotations
 
@@ -31,8 +35,8 @@ from typing import Dict, List, Optional, Tuple, Union
 import torch
 
 from .. import ops
-from ._core import (COMPACTATTN_VERSION, INDEXED_IMPLS, StageTimer, aligned_head, attend, check_attention_mask,
-                    dense_tables, dense_tail, geometry, kv_layouts, table_stats)
+from ._core import (COMPACTATTN_VERSION, INDEXED_IMPLS, StageTimer, attend, check_attention_mask, dense_tables,
+                    dense_tail, geometry, kv_layouts, starts_mid_block, table_stats)
 
 PACK_IMPLS = frozenset({"torch", "triton", "indexed_dense"})
 CACHE_FILL_BACKENDS = frozenset({"auto", "cuda", "triton"})
@@ -107,25 +111,16 @@ def _validate_impls(pack_impl: str, indexed_impl: str, cache_fill_backend: str) 
         raise ValueError(f"Unsupported cache_fill_backend: {cache_fill_backend}")
 
 
-def _split_unaligned(query_states, key_states, value_states, attention_mask, k_hf, v_hf, kv_len: int,
-                     num_kv_heads: int, head: int, softmax_scale, head_call, return_stats: bool):
-    """A call that is not block-aligned (aligned_head): fewer than 64 queries attend densely to
-    the whole KV; otherwise the block-aligned head runs through the entry (head_call(keep), over
-    the first `keep` keys) and the last q_len % 64 queries attend densely (dense_tail).  The
-    reference pads the partial block instead (attention_forward_chunked_dense.py:438-491) or
-    runs the whole call dense (:2396-2435)."""
+def _dense_mid_block(query_states, key_states, value_states, attention_mask, k_hf, v_hf, kv_len: int,
+                     num_kv_heads: int, softmax_scale, return_stats: bool):
+    """A chunk of at most 64 queries that starts inside a block attends densely to all kv_len
+    keys (dense_tail); no selection can align its query block with the key blocks."""
     check_attention_mask(attention_mask, query_states.shape[0], kv_len)
     K, V = kv_layouts(key_states, value_states, k_hf, v_hf)
-    q_len = query_states.shape[1]
-    stats: Optional[Dict[str, float]] = {"compactattn_version": COMPACTATTN_VERSION} if return_stats else None
-    parts = []
-    if head > 0:
-        out_head, stats = head_call(kv_len - (q_len - head))
-        parts.append(out_head)
-    parts.append(dense_tail(query_states[:, head:], K, V, kv_len, num_kv_heads, softmax_scale))
-    if stats is not None:
-        stats["col_dense_tail_tokens"] = float(q_len - head)
-    return (torch.cat(parts, dim=1) if len(parts) > 1 else parts[0]), stats
+    out = dense_tail(query_states, K, V, kv_len, num_kv_heads, softmax_scale)
+    if not return_stats:
+        return out, None
+    return out, {"compactattn_version": COMPACTATTN_VERSION, "col_dense_tail_tokens": float(query_states.shape[1])}
 
 
 def chunked_prefill_column_dense_attention_forward(
@@ -174,20 +169,9 @@ def chunked_prefill_column_dense_attention_forward(
     num_kv_heads = k_hf.shape[1] if k_hf is not None else key_states.shape[2]
     if query_states.dim() == 4 and query_states.shape[1] != query_length:
         raise ValueError(f"query_length={query_length} does not match query_states ({query_states.shape[1]})")
-    head = aligned_head(query_states.shape[1], kv_len) if block_size == 64 else None
-    if head is not None:
-        def head_call(keep):
-            cut = lambda t, dim: None if t is None else t.narrow(dim, 0, keep)  # noqa: E731
-            gate = attn_gate_score[:, :, :head // 64, :keep // 64]
-            return chunked_prefill_column_dense_attention_forward(
-                query_states[:, :head], cut(key_states, 1), cut(value_states, 1), cut(attention_mask, 1), head,
-                softmax_scale=softmax_scale, attn_gate_score=gate, threshold=threshold,
-                keep_recent_blocks=keep_recent_blocks, block_size=block_size,
-                num_key_value_groups=num_key_value_groups, attn_gate_is_kv_group_aware=attn_gate_is_kv_group_aware,
-                pack_impl=pack_impl, indexed_impl=indexed_impl, cache_fill_backend=cache_fill_backend,
-                return_stats=return_stats, k_hf=cut(k_hf, 2), v_hf=cut(v_hf, 2))
-        return _split_unaligned(query_states, key_states, value_states, attention_mask, k_hf, v_hf, kv_len,
-                                num_kv_heads, head, softmax_scale, head_call, return_stats)
+    if block_size == 64 and starts_mid_block(query_states.shape[1], kv_len):
+        return _dense_mid_block(query_states, key_states, value_states, attention_mask, k_hf, v_hf, kv_len,
+                                num_kv_heads, softmax_scale, return_stats)
     geo = geometry(query_states, kv_len, num_kv_heads, block_size)
     if geo.q_len != query_length:
         raise ValueError(f"query_length={query_length} does not match query_states ({geo.q_len})")
@@ -276,19 +260,9 @@ def chunked_prefill_column_dense_attention_from_keep_block(
     num_kv_heads = k_hf.shape[1] if k_hf is not None else key_states.shape[2]
     if query_states.dim() == 4 and query_states.shape[1] != query_length:
         raise ValueError(f"query_length={query_length} does not match query_states ({query_states.shape[1]})")
-    head = aligned_head(query_states.shape[1], kv_len) if block_size == 64 else None
-    if head is not None:
-        def head_call(keep):
-            cut = lambda t, dim: None if t is None else t.narrow(dim, 0, keep)  # noqa: E731  (tokens)
-            cutb = lambda t: None if t is None else t.narrow(2, 0, keep // 64)  # noqa: E731  (key blocks)
-            return chunked_prefill_column_dense_attention_from_keep_block(
-                query_states[:, :head], cut(key_states, 1), cut(value_states, 1), cutb(keep_block),
-                cut(attention_mask, 1), head, softmax_scale, block_size=block_size,
-                num_key_value_groups=num_key_value_groups, pack_impl=pack_impl, indexed_impl=indexed_impl,
-                cache_fill_backend=cache_fill_backend, return_stats=return_stats, valid_block=cutb(valid_block),
-                keep_block_kv_preprojected=cutb(keep_block_kv_preprojected), k_hf=cut(k_hf, 2), v_hf=cut(v_hf, 2))
-        return _split_unaligned(query_states, key_states, value_states, attention_mask, k_hf, v_hf, kv_len,
-                                num_kv_heads, head, softmax_scale, head_call, return_stats)
+    if block_size == 64 and starts_mid_block(query_states.shape[1], kv_len):
+        return _dense_mid_block(query_states, key_states, value_states, attention_mask, k_hf, v_hf, kv_len,
+                                num_kv_heads, softmax_scale, return_stats)
     geo = geometry(query_states, kv_len, num_kv_heads, block_size)
     if geo.q_len != query_length:
         raise ValueError(f"query_length={query_length} does not match query_states ({geo.q_len})")

@@ -11,31 +11,94 @@ blocks with non-causal and non-finite entries read as 0 (torch.topk over the zer
 last_n_block query blocks stay out of the union; the current chunk is always kept; then
 the GQA union, int32 block tables and the indexed attention.
 
+Score blocks are 64 or 128 tokens (block_size; 128 is the reference's default).  Pages,
+tables and attention stay in 64-token blocks: 128-token scoring pools pairs of 64-token
+summaries (ca_pair_block_summaries), applies the rule in 128-token block units (sink, window,
+min_budget and last_n_block count 128-token blocks, as in the reference) and names both
+64-token pages of every selected 128-token block.  A 128-token chunk must start at a multiple
+of 128 tokens.
+
 Scores are the pooled softmax of flash_prefill_score_chunked_from_mean_k (see
 compactattention_amd.flashprefill_vendor).  A first chunk (kv_len == q_len) runs dense causal
-attention on the same HIP kernel (identity tables), and a call with fewer than 64 queries
-attends densely through the decode kernel, where the reference calls its dense backend
-(q_len <= 1 or kv_len <= q_len, :903-907).  A longer chunk whose length is not a multiple of
-64 selects for its block-aligned head and runs its last q_len % 64 queries densely.
+attention on the same HIP kernel (identity tables); q_len <= 1 attends densely through the
+decode kernel, where the reference calls its dense backend (q_len <= 1 or kv_len <= q_len,
+:903-907).  A chunk whose length is not a multiple of the block size selects and attends with
+a partial last block (its summaries pool its valid tokens); one that starts inside a 64-token
+block (after decode steps) attends densely (at most 64 queries).
 """
 from __future__ import annotations
 
 import math
-from typing import Dict, Optional, Tuple
+from typing import Dict, Optional, Sequence, Tuple
 
 import torch
 
 from .. import ops
 from ..flashprefill_vendor import mean_k_kernel_layout
-from ._core import (COMPACTATTN_VERSION, INDEXED_IMPLS, StageTimer, aligned_head, attend, check_attention_mask,
-                    dense_tables, dense_tail, geometry, kv_layouts, table_stats)
+from ._core import (COMPACTATTN_VERSION, INDEXED_IMPLS, StageTimer, attend, check_attention_mask, dense_tables,
+                    dense_tail, geometry, kv_layouts, starts_mid_block, table_stats)
 from .attention_forward_chunked_dense import CACHE_FILL_BACKENDS, PACK_IMPLS
+
+SCORE_BLOCK_SIZES = (64, 128)
 
 
 def flashprefill_rule(attention_sink: int, window_size: int, alpha: float, last_n_block: int,
                       min_budget: int) -> ops.Rule:
     return ops.Rule(topk=max(int(min_budget), 0), alpha=float(alpha), sink_blocks=int(attention_sink),
                     window_blocks=int(window_size), last_n_block=int(last_n_block), topk_all_columns=True)
+
+
+def check_score_block_size(block_size: int) -> None:
+    if block_size not in SCORE_BLOCK_SIZES:
+        raise ValueError(f"block_size={block_size}: FlashPrefill scoring runs 64- or 128-token blocks")
+
+
+def expand_pair_tables(table: torch.Tensor, counts: torch.Tensor, key_blocks: int, kv_cap: int
+                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Tables of 128-token blocks -> tables of 64-token pages: block k names pages 2k and 2k + 1,
+    in order; when key_blocks (the 64-token blocks of each row) is odd, the last 128-token block
+    (the current chunk's, closing every row) has page 2k only.  Entries past the counts are -1."""
+    rows = table.shape[0]
+    t = table.to(torch.int64)
+    pages = torch.stack([2 * t, 2 * t + 1], dim=-1).reshape(rows, -1)
+    cnt = 2 * counts.to(torch.int64) - (key_blocks % 2)
+    out = torch.full((rows, kv_cap), -1, dtype=torch.int32, device=table.device)
+    width = min(kv_cap, pages.shape[1])
+    keep = torch.arange(width, device=table.device)[None, :] < cnt[:, None]
+    out[:, :width] = torch.where(keep, pages[:, :width], torch.full_like(pages[:, :width], -1)).to(torch.int32)
+    return out, cnt.to(torch.int32)
+
+
+def flashprefill_tables(qhat: torch.Tensor, khat: torch.Tensor, past_blocks: Sequence[int], q_len: int,
+                        num_kv_heads: int, kv_cap: int, rule: ops.Rule, block_size: int,
+                        khat_block_size: int = 64) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-KV-group tables of 64-token page ids for a chunk of q_len tokens at past_blocks
+    (64-token blocks, one value for every request).  qhat [B, Hq, ceil(q_len/64), 128] are the
+    chunk's 64-token query means; khat [B, Hkv, >= P + Qb, 128] the key means in
+    khat_block_size-token blocks (a 128-token khat goes straight to the 128-token scoring)."""
+    check_score_block_size(block_size)
+    scale = 1.0 / math.sqrt(128)
+    P = [int(p) for p in past_blocks]
+    if block_size == 64:
+        rowmask, _ = ops.score_select(qhat, khat, scale, rule, P, num_kv_heads, kv_cap)
+        table, counts, _, _ = ops.union_compact(rowmask, P, num_kv_heads, kv_cap, last_n_block=rule.last_n_block)
+        return table, counts
+    if len(set(P)) != 1 or P[0] % 2:
+        raise ValueError(f"128-token FlashPrefill blocks need a chunk that starts at a multiple of 128 tokens "
+                         f"(past {64 * P[0]} tokens)")
+    qb64 = qhat.shape[2]
+    last = q_len - 64 * (qb64 - 1)  # tokens of the chunk's last 64-token block
+    kb64 = P[0] + qb64
+    q128 = ops.pair_block_summaries(qhat, qb64, last)
+    P128 = [P[0] // 2] * len(P)
+    cap128 = -(-kb64 // 2)
+    if khat_block_size == 128:  # rows of exactly cap128 summaries (the kernels' row stride)
+        k128 = khat[..., :cap128, :].contiguous()
+    else:
+        k128 = ops.pair_block_summaries(khat, kb64, last)
+    rowmask, _ = ops.score_select(q128, k128, scale, rule, P128, num_kv_heads, cap128)
+    t128, c128, _, _ = ops.union_compact(rowmask, P128, num_kv_heads, cap128, last_n_block=rule.last_n_block)
+    return expand_pair_tables(t128, c128, kb64, kv_cap)
 
 
 def flashprefill_compactattn_prefill_full_kv(
@@ -68,31 +131,18 @@ def flashprefill_compactattn_prefill_full_kv(
         raise ValueError(f"Unsupported pack_impl: {pack_impl}")
     if cache_fill_backend not in CACHE_FILL_BACKENDS:
         raise ValueError(f"Unsupported cache_fill_backend: {cache_fill_backend}")
+    check_score_block_size(block_size)
     kv_len = k_hf.shape[2] if k_hf is not None else key_states.shape[1]
     num_kv_heads = k_hf.shape[1] if k_hf is not None else key_states.shape[2]
-    head = aligned_head(query_states.shape[1], kv_len) if block_size == 64 else None
-    if head is not None:
-        # fewer than 64 queries: dense over the whole KV (the reference's dense fallback for
-        # q_len <= 1, :903-907); otherwise the aligned head selects and the tail is dense
+    q_len = query_states.shape[1]
+    if q_len <= 1 or starts_mid_block(q_len, kv_len):
+        # the reference's dense fallback for q_len <= 1 (:903-907); a chunk starting inside a block
         check_attention_mask(attention_mask, query_states.shape[0], kv_len)
         K, V = kv_layouts(key_states, value_states, k_hf, v_hf)
-        stats: Dict[str, float] = {"compactattn_version": COMPACTATTN_VERSION}
-        parts = []
-        if head > 0:
-            keep = kv_len - (query_states.shape[1] - head)
-            cut = lambda t, dim: None if t is None else t.narrow(dim, 0, keep)  # noqa: E731
-            out_head, stats = flashprefill_compactattn_prefill_full_kv(
-                query_states[:, :head], cut(key_states, 1), cut(value_states, 1), cut(attention_mask, 1),
-                softmax_scale=softmax_scale, num_key_value_groups=num_key_value_groups, block_size=block_size,
-                attention_sink=attention_sink, window_size=window_size, alpha=alpha, last_n_block=last_n_block,
-                min_budget=min_budget, pack_impl=pack_impl, indexed_impl=indexed_impl,
-                cache_fill_backend=cache_fill_backend, measure_timing=measure_timing, k_hf=cut(k_hf, 2),
-                v_hf=cut(v_hf, 2), mean_k_cache=mean_k_cache)
-            parts.append(out_head)
-        parts.append(dense_tail(query_states[:, head:], K, V, kv_len, num_kv_heads, softmax_scale))
-        stats["flashprefill_dense_tail_tokens"] = float(query_states.shape[1] - head)
-        return torch.cat(parts, dim=1) if len(parts) > 1 else parts[0], stats
-    geo = geometry(query_states, kv_len, num_kv_heads, block_size)
+        out = dense_tail(query_states, K, V, kv_len, num_kv_heads, softmax_scale)
+        return out, {"compactattn_version": COMPACTATTN_VERSION, "flashprefill_dense_calls": 1.0,
+                     "flashprefill_dense_tail_tokens": float(q_len)}
+    geo = geometry(query_states, kv_len, num_kv_heads, 64)
     if geo.group != num_key_value_groups:
         raise ValueError(f"num_key_value_groups={num_key_value_groups} does not match heads "
                          f"{geo.num_q_heads}/{geo.num_kv_heads}")
@@ -108,32 +158,35 @@ def flashprefill_compactattn_prefill_full_kv(
         stats["flashprefill_dense_calls"] = 1.0
         stats.update(timer.results())
         return out, stats
+    if block_size == 128 and geo.past_blocks % 2:
+        raise ValueError(f"128-token FlashPrefill blocks need a chunk that starts at a multiple of 128 tokens "
+                         f"(past {kv_len - q_len} tokens)")
 
     def summaries():
+        """Key means in 64-token blocks, or the caller's mean_k_cache in block_size blocks."""
         if mean_k_cache is not None:
             m = mean_k_kernel_layout(mean_k_cache)
-            if m.shape[2] < geo.kv_cap:
-                raise ValueError(f"mean_k_cache covers {m.shape[2]} blocks, need {geo.kv_cap}")
-            return m
+            need = -(-kv_len // block_size)
+            if m.shape[2] < need:
+                raise ValueError(f"mean_k_cache covers {m.shape[2]} blocks, need {need}")
+            return m, block_size
         # no cache: block means of the whole key range (what the reference recomputes too)
         m = torch.empty((geo.batch, geo.num_kv_heads, geo.kv_cap, 128), dtype=torch.float32,
                         device=query_states.device)
         ks = key_states if key_states is not None else k_hf.transpose(1, 2)
         ops.cache_fill(ks, None, None, None, [0] * geo.batch, geo.kv_cap, m)
-        return m
+        return m, 64
 
-    khat = timer("mean_k_ms", summaries)
+    khat, khat_bs = timer("mean_k_ms", summaries)
     rule = flashprefill_rule(attention_sink, window_size, alpha, last_n_block, min_budget)
 
     def select():
-        qhat = ops.pool_query(query_states, P, khat.shape[2], num_kv_heads=geo.num_kv_heads)
-        rowmask, _ = ops.score_select(qhat, khat, 1.0 / math.sqrt(128), rule, P, geo.num_kv_heads,
-                                      khat.shape[2])
-        return rowmask
+        cap = khat.shape[2] if khat_bs == 64 else geo.kv_cap
+        qhat = ops.pool_query(query_states, P, cap, num_kv_heads=geo.num_kv_heads)
+        return flashprefill_tables(qhat, khat, P, geo.q_len, geo.num_kv_heads, cap, rule, block_size,
+                                   khat_block_size=khat_bs)
 
-    rowmask = timer("flashprefill_select_ms", select)
-    table, counts, _, _ = timer("flashprefill_union_ms", lambda: ops.union_compact(
-        rowmask, P, geo.num_kv_heads, khat.shape[2], last_n_block=last_n_block))
+    table, counts = timer("flashprefill_select_ms", select)
     out = timer("attention_ms", lambda: attend(query_states, K, V, table, counts, geo, softmax_scale))
     if measure_timing:
         stats.update(timer.results())

@@ -196,10 +196,11 @@ def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Opti
     vn = seq_layout(v_new, "v_new") if k_cache is not None else None
     if vn is not None and tuple(v_new.shape) != tuple(k_new.shape):
         raise ValueError("v_new must have k_new's shape")
-    blocks = max(int(p) for p in past_blocks) + Lq // BLOCK  # highest block written + 1
+    blocks = max(int(p) for p in past_blocks) + -(-Lq // BLOCK)  # highest block written + 1
+    tokens = BLOCK * max(int(p) for p in past_blocks) + Lq  # a partial last block writes its Lq % 64 rows
     for name, kv in (("k", k_cache), ("v", v_cache)):
         if kv is not None:
-            kv.check_blocks(name, B, Hkv, blocks)
+            kv.check_blocks(name, B, Hkv, blocks, tokens=tokens)
     if kmean is not None:
         _need_cuda("kmean", kmean, torch.float32)
         if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
@@ -228,7 +229,7 @@ def cache_fill(k_new: torch.Tensor, v_new: Optional[torch.Tensor], k_cache: Opti
 def pool_query(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, gate_wq: Optional[torch.Tensor] = None,
                rope_cos: Optional[torch.Tensor] = None, rope_sin: Optional[torch.Tensor] = None,
                num_kv_heads: Optional[int] = None) -> torch.Tensor:
-    """[B, Lq, Hq, 128] bf16 -> qhat [B, Hq, Lq/64, 128] fp32."""
+    """[B, Lq, Hq, 128] bf16 -> qhat [B, Hq, ceil(Lq/64), 128] fp32."""
     B, Lq, Hq, _ = q.shape
     d = make_dims(B, Lq, Hq, num_kv_heads or Hq, kv_cap)
     ql = seq_layout(q, "q")
@@ -241,7 +242,7 @@ def pool_query(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: int, gate_wq
             _need_cuda("rope_cos", rope_cos, torch.float32)
             _need_cuda("rope_sin", rope_sin, torch.float32)
             rope_rows = rope_cos.shape[0]
-    qhat = torch.empty((B, Hq, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
+    qhat = torch.empty((B, Hq, -(-Lq // BLOCK), HEAD_DIM), dtype=torch.float32, device=q.device)
     check(_hip.lib().ca_pool_query(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks, d.batch), _ptr(gate_wq),
                                    _ptr(rope_cos), _ptr(rope_sin), rope_rows, qhat.data_ptr(), _stream()))
     return qhat
@@ -251,7 +252,7 @@ def cache_fill_pool_query(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV,
                           past_blocks: Sequence[int], kv_cap: int, kmean: torch.Tensor,
                           q: torch.Tensor) -> torch.Tensor:
     """cache_fill(k_new, v_new, k_cache, v_cache, past_blocks, kv_cap, kmean) and
-    pool_query(q, past_blocks, kv_cap) in one launch; returns qhat [B, Hq, Lq/64, 128] fp32."""
+    pool_query(q, past_blocks, kv_cap) in one launch; returns qhat [B, Hq, ceil(Lq/64), 128] fp32."""
     B, Lq, Hkv, _ = k_new.shape
     Hq = q.shape[2]
     if tuple(q.shape[:2]) != (B, Lq) or tuple(v_new.shape) != tuple(k_new.shape):
@@ -260,13 +261,14 @@ def cache_fill_pool_query(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: KV,
         raise ValueError(f"num_q_heads={Hq} must be a multiple of num_kv_heads={Hkv}")
     d = make_dims(B, Lq, Hq, Hkv, kv_cap)
     kn, vn, ql = seq_layout(k_new, "k_new"), seq_layout(v_new, "v_new"), seq_layout(q, "q")
-    blocks = max(int(p) for p in past_blocks) + Lq // BLOCK
-    k_cache.check_blocks("k", B, Hkv, blocks)
-    v_cache.check_blocks("v", B, Hkv, blocks)
+    blocks = max(int(p) for p in past_blocks) + -(-Lq // BLOCK)
+    tokens = BLOCK * max(int(p) for p in past_blocks) + Lq
+    k_cache.check_blocks("k", B, Hkv, blocks, tokens=tokens)
+    v_cache.check_blocks("v", B, Hkv, blocks, tokens=tokens)
     _need_cuda("kmean", kmean, torch.float32)
     if not kmean.is_contiguous() or kmean.numel() < B * Hkv * kv_cap * HEAD_DIM:
         raise ValueError("kmean must be contiguous [B*Hkv, kv_cap, 128] fp32")
-    qhat = torch.empty((B, Hq, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
+    qhat = torch.empty((B, Hq, -(-Lq // BLOCK), HEAD_DIM), dtype=torch.float32, device=q.device)
     check(_hip.lib().ca_cache_fill_pool_query(ctypes.byref(d), ctypes.byref(kn), ctypes.byref(vn),
                                               ctypes.byref(k_cache.layout), ctypes.byref(v_cache.layout),
                                               past_array(past_blocks, d.batch), kmean.data_ptr(), ctypes.byref(ql),
@@ -319,7 +321,7 @@ def gate_query_summaries(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: in
                          gate_wq: Optional[torch.Tensor], num_kv_heads: int,
                          rope_cos: Optional[torch.Tensor] = None,
                          rope_sin: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """AttnGate query summaries: [B, Lq, Hq, 128] bf16 -> [B, gate_heads, Lq/64, 128] fp32.
+    """AttnGate query summaries: [B, Lq, Hq, 128] bf16 -> [B, gate_heads, ceil(Lq/64), 128] fp32.
     gate_wq None: one pool, no projection (gate_heads = Hq).  gate_wq [Hq, C*128, 128]: per
     Q head.  gate_wq [Hkv, G*C*128, 128]: the kv-group-aware form (the group's G heads
     pooled and concatenated head-major, one output per KV head)."""
@@ -337,11 +339,37 @@ def gate_query_summaries(q: torch.Tensor, past_blocks: Sequence[int], kv_cap: in
             raise ValueError(f"gate_wq must be contiguous [{gh}, {width}, {HEAD_DIM}] fp32")
     rows = _rope_args(rope_cos, rope_sin)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
-    qhat = torch.empty((B, gh, Lq // BLOCK, HEAD_DIM), dtype=torch.float32, device=q.device)
+    qhat = torch.empty((B, gh, -(-Lq // BLOCK), HEAD_DIM), dtype=torch.float32, device=q.device)
     check(_hip.lib().ca_gate_query_summaries(ctypes.byref(d), ctypes.byref(ql), past_array(past_blocks, d.batch),
                                              int(pools), _ptr(gate_wq), gh, _ptr(rope_cos), _ptr(rope_sin), rows,
                                              qhat.data_ptr(), _stream()))
     return qhat
+
+
+def pair_block_summaries(src: torch.Tensor, n_blocks: int, last_tokens: int,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """64-token summaries [..., >= n_blocks, 128] fp32 (the last of the n_blocks holding
+    last_tokens tokens) -> 128-token summaries [..., ceil(n_blocks/2), 128]:
+    (c0 m0 + c1 m1) / (c0 + c1) per pair, an unpaired last block copied."""
+    _need_cuda("src", src, torch.float32)
+    if src.dim() < 2 or src.shape[-1] != HEAD_DIM or src.shape[-2] < n_blocks or src.stride(-1) != 1 \
+            or src.stride(-2) != HEAD_DIM:
+        raise ValueError("src must be [..., >= n_blocks, 128] with contiguous summaries")
+    lead = src.shape[:-2]
+    rows = 1
+    for n in lead:
+        rows *= int(n)
+    src_rows = src.reshape(rows, src.shape[-2], HEAD_DIM)  # a view for the layouts the callers pass
+    npairs = -(-int(n_blocks) // 2)
+    if out is None:
+        out = torch.empty((*lead, npairs, HEAD_DIM), dtype=torch.float32, device=src.device)
+    dst_rows = out.reshape(rows, out.shape[-2], HEAD_DIM)
+    if dst_rows.data_ptr() != out.data_ptr() or out.shape[-2] < npairs:
+        raise ValueError("out must be contiguous [..., >= ceil(n_blocks/2), 128]")
+    check(_hip.lib().ca_pair_block_summaries(src_rows.data_ptr(), src_rows.stride(0) // HEAD_DIM,
+                                             dst_rows.data_ptr(), dst_rows.stride(0) // HEAD_DIM, rows,
+                                             int(n_blocks), int(last_tokens), _stream()))
+    return out
 
 
 def words_for(kv_cap: int) -> int:
@@ -385,8 +413,8 @@ def select_scores(scores: torch.Tensor, rule: Rule, past_blocks: Sequence[int], 
     if scores.dim() != 4 or scores.stride(-1) != 1:
         raise ValueError("scores must be [B, Hq, Qb, Kb] with a contiguous last dim")
     B, Hq, Qb, Kb = scores.shape
-    if Qb != q_len // BLOCK:
-        raise ValueError(f"scores have {Qb} query blocks, expected {q_len // BLOCK}")
+    if Qb != -(-q_len // BLOCK):
+        raise ValueError(f"scores have {Qb} query blocks, expected {-(-q_len // BLOCK)}")
     if Kb < max(int(p) for p in past_blocks) + Qb:
         raise ValueError("scores have fewer key blocks than past + current blocks")
     d = make_dims(B, q_len, Hq, num_kv_heads, kv_cap)
@@ -503,9 +531,10 @@ def attn_fwd(q: torch.Tensor, k: KV, v: KV, table: torch.Tensor, counts: torch.T
         raise ValueError("table must be [B*Hkv, >= kv_cap] with contiguous rows")
     if counts.numel() < B * num_kv_heads:
         raise ValueError("counts must hold B*Hkv entries")
-    blocks = max(int(p) for p in past_blocks) + Lq // BLOCK  # blocks a row's table may name
+    blocks = max(int(p) for p in past_blocks) + -(-Lq // BLOCK)  # blocks a row's table may name
+    tokens = BLOCK * max(int(p) for p in past_blocks) + Lq  # reads stop at each request's 64 P + Lq
     for name, kv in (("k", k), ("v", v)):
-        kv.check_blocks(name, B, num_kv_heads, blocks)
+        kv.check_blocks(name, B, num_kv_heads, blocks, tokens=tokens)
     d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
     pa = past_array(past_blocks, d.batch)
     # num_splits = 0 hands the choice to the library

@@ -51,8 +51,10 @@ class SeerAttnLlamaConfig:
     seerattn_compactattn_keep_recent_blocks: int = 2
     compactattn_sink_blocks: int = 0
     compactattn_local_blocks: int = 0
-    # FlashPrefill selector (modeling_llama_flashprefill_compactattn.py:266-293)
-    seerattn_flashprefill_block_size: int = 64
+    # FlashPrefill selector (modeling_llama_flashprefill_compactattn.py:253,266-293,486-491): score
+    # blocks of 128 tokens by default as in the reference (64 or 128 here); BASELINE's FlashPrefill
+    # configurations score 64-token blocks
+    seerattn_flashprefill_block_size: int = 128
     seerattn_flashprefill_attention_sink: int = 2
     seerattn_flashprefill_window_size: int = 4
     seerattn_flashprefill_alpha: float = 0.06
@@ -79,8 +81,10 @@ class SeerAttnLlamaConfig:
             raise ValueError("the compactattn kernels run head_dim 128")
         if self.num_attention_heads % self.num_key_value_heads:
             raise ValueError("num_attention_heads must be a multiple of num_key_value_heads")
-        if self.seerattn_gate_block_size != 64 or self.seerattn_flashprefill_block_size != 64:
+        if self.seerattn_gate_block_size != 64:
             raise ValueError("the compactattn path runs 64-token blocks")
+        if self.seerattn_flashprefill_block_size not in (64, 128):
+            raise ValueError("FlashPrefill scoring runs 64- or 128-token blocks")
         from ..attn_gate import parse_gate_type
 
         parse_gate_type(self.seerattn_gate_type)

@@ -187,29 +187,13 @@ def dense_decode_forward(attn: nn.Module, hidden_states: torch.Tensor, position_
     return attn.o_proj(out.reshape(B, L, -1))
 
 
-def split_unaligned_chunk(attn: nn.Module, hidden_states: torch.Tensor, position_embeddings, past_key_value,
-                          attention_mask=None, **kwargs):
-    """A chunk of 64*n + r tokens (n >= 1, 0 < r < 64) over a block-aligned cache, e.g. the
-    last chunk of a prompt whose length is not a multiple of 64: its first 64*n tokens take
-    the module's chunk path (selection over whole blocks), then its last r tokens are one
-    dense step over the whole cache through the decode kernel (which reads the partial last
-    block up to the cache length only).  The reference instead pads the partial block and
-    keeps it selected for the whole chunk (compact_attn/modules/
-    attention_forward_chunked_dense.py:438-491); here the tail queries attend to every cached
-    key.  Returns the module's 5-tuple with the two parts' outputs concatenated."""
-    L = hidden_states.shape[1]
-    head_len = L - L % BLOCK
-    cos, sin = position_embeddings
-    head = attn.forward(hidden_states[:, :head_len], (cos[:head_len], sin[:head_len]), attention_mask,
-                        past_key_value=past_key_value, **kwargs)[0]
-    tail = dense_decode_forward(attn, hidden_states[:, head_len:], (cos[head_len:], sin[head_len:]),
-                                past_key_value.layer(attn.layer_idx))
-    return torch.cat([head, tail], dim=1), 0.0, None, None, None
-
-
 def is_decode_step(hidden_states: torch.Tensor, cache: PagedKVCache) -> bool:
-    """Fewer than 64 new tokens, or a cache already past a block boundary, is decode."""
-    return hidden_states.shape[1] < BLOCK or cache.length % BLOCK != 0
+    """One new token, or a cache already past a block boundary (decode steps left it inside a
+    block), is a dense decode step; any other call of two or more tokens is a chunk that
+    selects (the reference's chunked_prefill = q_len > 1 and kv_len > q_len,
+    compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:622-640),
+    whatever its length: a chunk that is not a multiple of 64 tokens ends in a partial block."""
+    return hidden_states.shape[1] == 1 or cache.length % BLOCK != 0
 
 
 class ChunkedPrefillCache:

@@ -12,11 +12,14 @@ chunk only appends, through ca_cache_fill); ca_score_select scores
 pooled Q.K blocks (softmax over causal key blocks, scale 1/sqrt(128)) and applies the
 FlashPrefill row rule (alpha * row max, sink, window, optional top-k budget);
 ca_union_compact leaves the last last_n_block query blocks out of the union; ca_attn_fwd
-attends over the cache pages.
+attends over the cache pages.  With seerattn_flashprefill_block_size 128 (the reference's
+default) the pooled query and key means are paired into 128-token blocks
+(ca_pair_block_summaries) before scoring, and the tables name both 64-token pages of each
+selected block.  A chunk that is not a multiple of 64 tokens selects with a partial last
+block.
 """
 from __future__ import annotations
 
-import math
 from typing import Optional, Tuple
 
 import torch
@@ -24,11 +27,10 @@ from torch import nn
 
 from ... import ops
 from ...modules._core import COMPACTATTN_VERSION
-from ...modules.flashprefill_prefill import flashprefill_rule
+from ...modules.flashprefill_prefill import flashprefill_rule, flashprefill_tables
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
-                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk,
-                                     split_unaligned_chunk)
+                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk)
 
 BLOCK = 64
 
@@ -74,8 +76,6 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
             self._compactattn_last_stats = {"path": "decode_dense"} if self.compactattn_debug else None
             return out, 0.0, None, None, None
         B, L, _ = hidden_states.shape
-        if L % BLOCK:
-            return split_unaligned_chunk(self, hidden_states, position_embeddings, past_key_value, attention_mask)
         q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
         with event_span(self.attention_timer):
@@ -90,12 +90,10 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
             if dense:
                 table, counts = ops.dense_table(P, L, self.num_heads, self.num_key_value_heads, cache.cap,
                                                 query_states.device)
-            else:
-                rule = self._selection_rule()
-                rowmask, _ = ops.score_select(qhat, cache.kmean, 1.0 / math.sqrt(self.head_dim), rule, P,
-                                              self.num_key_value_heads, cache.cap)
-                table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap,
-                                                        last_n_block=rule.last_n_block)
+            else:  # score blocks of seerattn_flashprefill_block_size (64 or 128) tokens
+                table, counts = flashprefill_tables(qhat, cache.kmean, P, L, self.num_key_value_heads, cache.cap,
+                                                    self._selection_rule(),
+                                                    self.config.seerattn_flashprefill_block_size)
             K, V = cache.layouts()
             out = ops.attn_fwd(query_states, K, V, table, counts, P, self.scaling, cache.cap,
                                self.num_key_value_heads)

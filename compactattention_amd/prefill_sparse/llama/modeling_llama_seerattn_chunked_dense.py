@@ -38,8 +38,7 @@ from ...modules.attention_forward_chunked_dense import (_compactattn_effective_t
 from ..attn_gate import ATTNGATE_CLASSES
 from .configuration_llama_seerattn import SeerAttnLlamaConfig
 from .modeling_llama_common import (ChunkedPrefillCache, CompactAttnLlamaForCausalLM, FusedProjections,
-                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk,
-                                     split_unaligned_chunk)
+                                     dense_decode_forward, event_span, is_decode_step, project_qkv, rope_qk)
 
 BLOCK = 64
 
@@ -141,7 +140,7 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         self.attn_gate.compress_key_blocks(key_states_nope, out=cache.kgate, first_block=past,
                                            position_embeddings=block_position_embeddings)
         if cache.kgate_blocks == past:  # a gap left by decode-completed blocks stays a gap
-            cache.kgate_blocks = past + key_states_nope.shape[1] // BLOCK
+            cache.kgate_blocks = past - (-key_states_nope.shape[1] // BLOCK)  # a partial block's summary counts
 
     def _select_tables(self, query_states_nope: torch.Tensor, cache, past: int, block_position_embeddings
                        ) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -152,7 +151,7 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
         gate = self.attn_gate
         qhat = gate.compress_query_blocks(query_states_nope, first_block=past,
                                           position_embeddings=block_position_embeddings, kv_cap=cache.cap)
-        q_blocks = query_states_nope.shape[1] // BLOCK
+        q_blocks = -(-query_states_nope.shape[1] // BLOCK)
         rule = self._selection_rule(q_blocks, 64 * past + query_states_nope.shape[1])
         rowmask, _ = ops.score_select(qhat, cache.kgate, gate.scale, rule, P, gate.key_heads, cache.cap)
         table, counts, _, _ = ops.union_compact(rowmask, P, self.num_key_value_heads, cache.cap)
@@ -187,9 +186,6 @@ class LlamaSeerAttentionChunkedDense(nn.Module):
             self._compactattn_last_stats = {"path": "decode_dense"} if self.compactattn_debug else None
             return out, 0.0, None, None, None
         B, L, _ = hidden_states.shape
-        if L % BLOCK:
-            return split_unaligned_chunk(self, hidden_states, position_embeddings, past_key_value, attention_mask,
-                                         block_position_embeddings=block_position_embeddings)
         q, k, v = project_qkv(self, hidden_states)
         cos, sin = position_embeddings
         with event_span(self.attention_timer):

@@ -65,11 +65,13 @@ enum {
 
 typedef struct {
     int32_t batch;        /* requests in the launch, <= CA_MAX_BATCH                 */
-    int32_t q_len;        /* chunk tokens per request, a multiple of 64              */
+    int32_t q_len;        /* chunk tokens per request; the chunk starts at a block
+                             boundary and covers Qb = ceil(q_len/64) blocks, the last
+                             holding q_len - 64 (Qb - 1) tokens                      */
     int32_t num_q_heads;  /* Hq                                                      */
     int32_t num_kv_heads; /* Hkv; Hq % Hkv == 0, group G = Hq / Hkv <= 16            */
     int32_t kv_cap;       /* per-row capacity in blocks of tables and summaries;
-                             >= past_blocks[b] + q_len/64 for every request          */
+                             >= past_blocks[b] + Qb for every request                */
 } ca_dims;
 
 typedef struct {
@@ -107,10 +109,18 @@ int ca_abi_version(void);
 const char* ca_last_error(void);
 
 /*
+ * Partial blocks.  A chunk whose q_len is not a multiple of 64 ends in a block of
+ * n = q_len - 64 (Qb - 1) tokens: its rows are the only ones read from the chunk's tensors
+ * and written to the cache (the cache rows past them keep what they held), and its
+ * summaries pool those n tokens -- max and min over them, avg = their sequential sum
+ * divided by n (the reference's mean over the valid tokens of a block,
+ * compact_attn/flashprefill_vendor/flashprefill_native_forward.py:44-95; the pooling of
+ * AttnGate's ceil_mode pools, compact_attn/prefill_sparse/attn_gate.py:113-130).
+ *
  * Cache fill.  Appends one chunk of K/V per request into the cache at logical blocks
- * [past_blocks[b], past_blocks[b] + q_len/64) and writes, for each new block, the fp32
- * mean of its 64 K rows into kmean[(b*Hkv + h)*kv_cap + kb][128] (sequential sum over the
- * 64 tokens, times 1/64).  If gate_wk is given ([Hkv, 128, 128], in x out) it also writes
+ * [past_blocks[b], past_blocks[b] + Qb) and writes, for each new block, the fp32
+ * mean of its K rows into kmean[(b*Hkv + h)*kv_cap + kb][128] (sequential sum over the
+ * block's tokens divided by their count, 64 except in a partial last block).  If gate_wk is given ([Hkv, 128, 128], in x out) it also writes
  * kgate = RoPE(W_k[h]^T mean) (rope_cos/rope_sin: [rope_rows, 128] indexed by absolute
  * block id, may be NULL for no RoPE) into kgate with the kmean layout.  With k_cache and
  * v_cache both NULL nothing is copied and only the summaries are written (v_new unused).
@@ -129,8 +139,8 @@ int ca_cache_fill(const ca_dims* dims, const ca_seq_layout* k_new, const ca_seq_
                   void* stream);
 
 /*
- * Pooled query summaries: qhat[(b*Hq + h)*Qb + qb][128] = mean of the 64 query rows of
- * block qb (sequential sum, times 1/64), optionally projected by gate_wq [Hq, 128, 128]
+ * Pooled query summaries: qhat[(b*Hq + h)*Qb + qb][128] = mean of the query rows of
+ * block qb (sequential sum divided by the block's token count), optionally projected by gate_wq [Hq, 128, 128]
  * and rotated at absolute block id past_blocks[b] + qb.
  * Replaces: AttnGate.compress_query_blocks + block RoPE (attn_gate.py:113-171) and the
  * query-side mean of compute_block_score_chunked (flashprefill_native_forward.py:98-207).
@@ -157,7 +167,7 @@ int ca_cache_fill_pool_query(const ca_dims* dims, const ca_seq_layout* k_new, co
  * AttnGate block summaries for every gate type of the reference (compact_attn/prefill_sparse/
  * attn_gate.py:37-130,233-278: the Q{pools}_K{pools} classes, force_double, the
  * kv_group_aware_query form).  pools is a set of CA_POOL_* bits; the pooled vectors of a
- * 64-token block (max and min of the bf16 values, avg = sequential sum times 1/64) are
+ * block (max and min of the bf16 values, avg = sequential sum divided by the token count) are
  * concatenated in the order max, min, avg into an input of in = C*128 values (C pools), then
  * projected, y[o] = sum_{i < in} x[i] W[i][o] (sequential fma over i), and rotated at the
  * block's absolute id (rope_cos/rope_sin [rope_rows, 128], may be NULL).
@@ -168,7 +178,7 @@ int ca_cache_fill_pool_query(const ca_dims* dims, const ca_seq_layout* k_new, co
  * heads of its group (head hk*G + j) and projected per Q head with W_k [Hq, in, 128] -- the
  * reference's single-linear gate (attn_gate.py:84-86 with MultiHeadLinear's repeat, :30-33).
  * ca_gate_query_summaries: the query blocks of q ([B, q_len, Hq, 128]) -> qhat
- * [B, gate_heads, q_len/64, 128].  gate_wq NULL: no projection (one pool only, gate_heads =
+ * [B, gate_heads, Qb, 128].  gate_wq NULL: no projection (one pool only, gate_heads =
  * num_q_heads; the pooled vector is still rotated when rope tables are given, as the
  * reference rotates its unprojected query blocks).  gate_heads = num_q_heads: W_q
  * [Hq, in, 128] per Q head.  gate_heads =
@@ -187,6 +197,23 @@ int ca_gate_key_summaries(const ca_dims* dims, const ca_seq_layout* k_new, const
 int ca_gate_query_summaries(const ca_dims* dims, const ca_seq_layout* q, const int32_t* past_blocks_host,
                             int32_t pools, const float* gate_wq, int32_t gate_heads, const float* rope_cos,
                             const float* rope_sin, int64_t rope_rows, float* qhat, void* stream);
+
+/*
+ * 128-token block summaries from 64-token ones, for FlashPrefill scoring with 128-token
+ * blocks (the reference's default block_size, compact_attn/prefill_sparse/llama/
+ * modeling_llama_flashprefill_compactattn.py:253; compact_attn/load_attention_replacement.py:
+ * 255), while pages, tables and attention stay in 64-token blocks.  For each of `rows` rows of
+ * n_blocks 64-token summaries (src [rows, src_stride, 128] fp32, the last block holding
+ * last_tokens tokens, 1..64) it writes ceil(n_blocks/2) summaries (dst [rows, dst_stride, 128]):
+ *     dst[j] = (c0 * src[2j] + c1 * src[2j+1]) / (c0 + c1)
+ * in fp32 (two products, their sum, one correctly rounded division), c the blocks' token
+ * counts, and dst[j] = src[2j] when 2j is the last block.  For block means this is the mean
+ * over the pair's tokens (compute_mean_vector's per-block mean at block_size 128,
+ * compact_attn/flashprefill_vendor/flashprefill_native_forward.py:44-95) up to rounding.
+ * No counterpart in _C_compactattn.
+ */
+int ca_pair_block_summaries(const float* src, int64_t src_stride, float* dst, int64_t dst_stride, int64_t rows,
+                            int32_t n_blocks, int32_t last_tokens, void* stream);
 
 /*
  * Block scoring and per-row selection.  For every (b, h, qb) row it computes

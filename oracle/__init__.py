@@ -125,11 +125,12 @@ def exp(x: np.ndarray) -> np.ndarray:
 
 
 def block_mean(x_bits: np.ndarray) -> np.ndarray:
-    """x: [B, L, H, 128] bf16 bits -> [B, H, L/64, 128] fp32 block means."""
+    """x: [B, L, H, 128] bf16 bits -> [B, H, ceil(L/64), 128] fp32 block means (a partial last
+    block averages its L % 64 tokens)."""
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     B, L, H, d = x.shape
-    assert d == D and L % BLOCK == 0
-    out = np.empty((B, H, L // BLOCK, D), dtype=np.float32)
+    assert d == D and L > 0
+    out = np.empty((B, H, -(-L // BLOCK), D), dtype=np.float32)
     lib().orc_block_mean(_p(x), B, L, H, _p(out))
     return out
 
@@ -149,13 +150,25 @@ def pool_bits(names) -> int:
 
 
 def block_pool(x_bits: np.ndarray, pools: int) -> np.ndarray:
-    """x: [B, L, H, 128] bf16 bits -> [B, H, L/64, C*128] fp32 (max, min, avg as selected)."""
+    """x: [B, L, H, 128] bf16 bits -> [B, H, ceil(L/64), C*128] fp32 (max, min, avg as selected;
+    a partial last block pools its L % 64 tokens)."""
     x = np.ascontiguousarray(x_bits, dtype=np.uint16)
     B, L, H, d = x.shape
-    assert d == D and L % BLOCK == 0 and 0 < pools < 8
+    assert d == D and L > 0 and 0 < pools < 8
     C = bin(pools).count("1")
-    out = np.empty((B, H, L // BLOCK, C * D), dtype=np.float32)
+    out = np.empty((B, H, -(-L // BLOCK), C * D), dtype=np.float32)
     lib().orc_block_pool(_p(x), B, L, H, int(pools), _p(out))
+    return out
+
+
+def pair_block_means(src: np.ndarray, last_tokens: int) -> np.ndarray:
+    """[..., n_blocks, 128] fp32 64-token summaries (the last block holding last_tokens tokens)
+    -> [..., ceil(n_blocks/2), 128] 128-token summaries."""
+    x = np.ascontiguousarray(src, dtype=np.float32)
+    lead, n = x.shape[:-2], x.shape[-2]
+    rows = int(np.prod(lead)) if lead else 1
+    out = np.empty(lead + (-(-n // 2), D), dtype=np.float32)
+    lib().orc_pair_block_means(_p(x), rows, n, int(last_tokens), _p(out))
     return out
 
 

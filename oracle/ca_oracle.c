@@ -91,34 +91,48 @@ float orc_exp(float x) {
     return p * bits_f32((uint32_t)(ni + 127) << 23);
 }
 
+/* Tokens of block n of a sequence of L tokens: 64, or L % 64 for a partial last block. */
+static int block_tokens(int L, int n) {
+    const int left = L - n * ORC_BLOCK;
+    return left < ORC_BLOCK ? left : ORC_BLOCK;
+}
+
+/* Block means follow compute_mean_vector (compact_attn/flashprefill_vendor/
+ * flashprefill_native_forward.py:44-95): the sum over the block's valid tokens divided by
+ * their count (64 except in a partial last block), summed here in token order. */
 void orc_block_mean(const uint16_t* x, int B, int L, int H, float* out) {
-    const int nb = L / ORC_BLOCK;
+    const int nb = (L + ORC_BLOCK - 1) / ORC_BLOCK;
     for (int b = 0; b < B; ++b)
         for (int h = 0; h < H; ++h)
-            for (int n = 0; n < nb; ++n)
+            for (int n = 0; n < nb; ++n) {
+                const int nv = block_tokens(L, n);
                 for (int d = 0; d < ORC_D; ++d) {
                     float s = 0.0f;
-                    for (int t = 0; t < ORC_BLOCK; ++t) {
+                    for (int t = 0; t < nv; ++t) {
                         const int64_t tok = (int64_t)n * ORC_BLOCK + t;
                         s = s + orc_bf16_to_f32(x[(((int64_t)b * L + tok) * H + h) * ORC_D + d]);
                     }
-                    out[(((int64_t)b * H + h) * nb + n) * ORC_D + d] = s * 0.015625f;
+                    out[(((int64_t)b * H + h) * nb + n) * ORC_D + d] = s / (float)nv;
                 }
+            }
 }
 
+/* AttnGate pools (attn_gate.py:113-130,233-237; ceil_mode pools cover a partial last block's
+ * valid tokens only). */
 void orc_block_pool(const uint16_t* x, int B, int L, int H, int pools, float* out) {
-    const int nb = L / ORC_BLOCK;
+    const int nb = (L + ORC_BLOCK - 1) / ORC_BLOCK;
     int C = 0;
     for (int bit = 1; bit <= ORC_POOL_AVG; bit <<= 1) C += (pools & bit) ? 1 : 0;
     for (int b = 0; b < B; ++b)
         for (int h = 0; h < H; ++h)
             for (int n = 0; n < nb; ++n) {
+                const int nv = block_tokens(L, n);
                 float* o = out + (((int64_t)b * H + h) * nb + n) * (int64_t)C * ORC_D;
                 for (int d = 0; d < ORC_D; ++d) {
                     const uint16_t* xs = x + ((((int64_t)b * L + (int64_t)n * ORC_BLOCK) * H) + h) * ORC_D + d;
                     const int64_t st = (int64_t)H * ORC_D;
                     float mx = orc_bf16_to_f32(xs[0]), mn = mx, s = 0.0f;
-                    for (int t = 0; t < ORC_BLOCK; ++t) {
+                    for (int t = 0; t < nv; ++t) {
                         const float v = orc_bf16_to_f32(xs[t * st]);
                         mx = v > mx ? v : mx;
                         mn = v < mn ? v : mn;
@@ -127,9 +141,37 @@ void orc_block_pool(const uint16_t* x, int B, int L, int H, int pools, float* ou
                     int c = 0;
                     if (pools & ORC_POOL_MAX) o[(c++) * ORC_D + d] = mx;
                     if (pools & ORC_POOL_MIN) o[(c++) * ORC_D + d] = mn;
-                    if (pools & ORC_POOL_AVG) o[(c++) * ORC_D + d] = s * 0.015625f;
+                    if (pools & ORC_POOL_AVG) o[(c++) * ORC_D + d] = s / (float)nv;
                 }
             }
+}
+
+/* 128-token summaries from pairs of 64-token ones: (c0*m0 + c1*m1) / (c0 + c1) in fp32 with the
+ * blocks' token counts (64, last_tokens for the last block); an unpaired last block is copied.
+ * The order (two products, their sum, one division) is the one the product's pair kernel
+ * uses. */
+void orc_pair_block_means(const float* src, int rows, int n_blocks, int last_tokens, float* dst) {
+    const int np = (n_blocks + 1) / 2;
+    for (int r = 0; r < rows; ++r)
+        for (int j = 0; j < np; ++j) {
+            const int b0 = 2 * j;
+            const float* m0 = src + ((int64_t)r * n_blocks + b0) * ORC_D;
+            float* o = dst + ((int64_t)r * np + j) * ORC_D;
+            if (b0 + 1 >= n_blocks) {
+                for (int d = 0; d < ORC_D; ++d) o[d] = m0[d];
+                continue;
+            }
+            const float* m1 = m0 + ORC_D;
+            const float c0 = b0 == n_blocks - 1 ? (float)last_tokens : 64.0f;
+            const float c1 = b0 + 1 == n_blocks - 1 ? (float)last_tokens : 64.0f;
+            const float n = c0 + c1;
+            for (int d = 0; d < ORC_D; ++d) {
+                const float a = c0 * m0[d];
+                const float b = c1 * m1[d];
+                const float t = a + b;
+                o[d] = t / n;
+            }
+        }
 }
 
 void orc_gate_project(const float* x, int B, int H, int N, const float* W,

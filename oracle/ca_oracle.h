@@ -47,7 +47,8 @@ float orc_exp(float x);
 float orc_bf16_to_f32(uint16_t v);
 uint16_t orc_f32_to_bf16(float v);
 
-/* x: [B, L, H, 128] bf16 (L % 64 == 0) -> out: [B, H, L/64, 128] fp32 block means. */
+/* x: [B, L, H, 128] bf16 -> out: [B, H, ceil(L/64), 128] fp32 block means: the sequential
+ * sum over a block's tokens divided by their count (64, or L % 64 for a partial last block). */
 void orc_block_mean(const uint16_t* x, int B, int L, int H, float* out);
 
 /* Gate pooling set (AttnGate pooling functions, compact_attn/prefill_sparse/attn_gate.py:
@@ -56,11 +57,17 @@ void orc_block_mean(const uint16_t* x, int B, int L, int H, float* out);
 #define ORC_POOL_MIN 2
 #define ORC_POOL_AVG 4
 
-/* Block pooling over 64 tokens: x [B, L, H, 128] bf16 -> out [B, H, L/64, C*128] fp32 with
- * C = popcount(pools); max and min keep the bf16 values, avg is the sequential sum times 1/64
- * (as orc_block_mean).  max/min are strict compares from token 0 (the first of equal values
+/* Block pooling: x [B, L, H, 128] bf16 -> out [B, H, ceil(L/64), C*128] fp32 with
+ * C = popcount(pools), over each block's tokens (a partial last block's valid ones); max and
+ * min keep the bf16 values, avg is as orc_block_mean.  max/min are strict compares from token 0 (the first of equal values
  * stays). */
 void orc_block_pool(const uint16_t* x, int B, int L, int H, int pools, float* out);
+
+/* 128-token summaries from 64-token ones (FlashPrefill with 128-token score blocks): src
+ * [rows, n_blocks, 128] (the last block holds last_tokens tokens) -> dst [rows,
+ * ceil(n_blocks/2), 128], dst[j] = (c0*src[2j] + c1*src[2j+1]) / (c0 + c1) (fp32: two products,
+ * their sum, one division; c = 64 or last_tokens), an unpaired last block copied. */
+void orc_pair_block_means(const float* src, int rows, int n_blocks, int last_tokens, float* dst);
 
 /* Per-head gate projection followed by block RoPE.
  * x: [B, H, N, 128] fp32, W: [H, 128, 128] (in, out), cos/sin: [rope_rows, 128]

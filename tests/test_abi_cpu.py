@@ -61,7 +61,8 @@ def _past(*p):
 @pytest.mark.parametrize("dims,past,code,msg", [
     (_dims(batch=0), (0,), _hip.CA_ERR_INVALID, "batch"),
     (_dims(batch=65), (0,), _hip.CA_ERR_LIMIT, "batch"),
-    (_dims(q_len=100), (0,), _hip.CA_ERR_INVALID, "multiple of 64"),
+    (_dims(q_len=0), (0,), _hip.CA_ERR_INVALID, "must be positive"),
+    (_dims(q_len=100, kv_cap=1), (0,), _hip.CA_ERR_INVALID, "exceeds kv_cap"),  # 100 tokens span 2 blocks
     (_dims(num_q_heads=7), (0,), _hip.CA_ERR_INVALID, "multiple"),
     (_dims(num_q_heads=34, num_kv_heads=2), (0,), _hip.CA_ERR_LIMIT, "group size"),
     (_dims(kv_cap=9), (8,), _hip.CA_ERR_INVALID, "exceeds kv_cap"),

@@ -230,74 +230,182 @@ def test_flashprefill_entry(gpu, params):
     _check_attention(out, ch, ref_table, ref_counts)
 
 
-@pytest.mark.parametrize("q_len", [1, 37, 256 + 37])
-def test_unaligned_entries(gpu, q_len):
-    """Calls whose q_len is not a multiple of 64 (the chunk starting on a block): fewer than 64
-    queries attend densely to all kv_len keys (the reference's dense fallback); a longer chunk
-    selects for its aligned head (the reference's tables over the head's keys) and its last
-    q_len % 64 queries attend densely -- for the FlashPrefill entry and both Seer entries."""
-    _print_case(test="unaligned_entries", q_len=q_len)
-    Hq, Hkv, past = 8, 2, 64 * 20
+def _pad_keys(x, cap):
+    """[B, K, H, D] -> heads-first [B, H, cap*64, D] with zero rows past K (never visible to a query)."""
+    out = torch.zeros((x.shape[0], x.shape[2], cap * 64, x.shape[3]), dtype=x.dtype)
+    out[:, :, :x.shape[1]] = x.transpose(1, 2)
+    return out
+
+
+@pytest.mark.parametrize("q_len", [37, 256 + 37])
+def test_unaligned_chunk_selects_with_a_partial_block(gpu, monkeypatch, q_len):
+    """A chunk of q_len tokens (not a multiple of 64) starting at a block boundary, through the
+    FlashPrefill entry and both Seer entries: ceil(q_len/64) query blocks whose last pools its
+    q_len % 64 tokens (as compute_mean_vector and AttnGate's ceil_mode pools do), key blocks up
+    to the partial last one, the reference's selection over them, the partial current block
+    kept, and every query row -- the tail queries included -- attending over the selected past
+    blocks and the current chunk with the causal mask at the true positions (the reference's
+    padded indexed path, attention_forward_chunked_dense.py:438-491, without its padded-length
+    causal alignment).  Tables bit-exact against the oracle's; every output row against the
+    fp64 oracle over those tables."""
+    _print_case(test="unaligned_chunk", q_len=q_len)
+    Hq, Hkv, past = 8, 2, 64 * 40
     G = Hq // Hkv
     kv_len = past + q_len
-    head = 0 if q_len < 64 else q_len - q_len % 64
+    P = [past // 64]
+    Qb = -(-q_len // 64)
+    cap = P[0] + Qb
     g = torch.Generator().manual_seed(q_len)
+    # block structure (a shared direction per query head, an offset per key block) makes the
+    # pooled scores selective
+    q = (torch.randn((1, q_len, Hq, 128), generator=g) + 3 * torch.randn((1, 1, Hq, 128), generator=g))
+    q = q.to(torch.bfloat16)
+    offs = 2 * torch.randn((1, cap, 1, Hkv, 128), generator=g).expand(1, cap, 64, Hkv, 128).reshape(1, cap * 64, Hkv, 128)
+    k = (torch.randn((1, kv_len, Hkv, 128), generator=g) + offs[:, :kv_len]).to(torch.bfloat16)
+    v = torch.randn((1, kv_len, Hkv, 128), generator=g).to(torch.bfloat16)
+    kp, vp = _pad_keys(k, cap), _pad_keys(v, cap)
+
+    def check(out, table, counts):
+        ref = oracle.attention(bits(q), bits(kp), bits(vp), P, table, counts, SCALE)
+        err = np.abs(f32(out) - ref)
+        assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
+        assert (counts < cap).any(), "the case should drop blocks"
+
+    calls = spy_union_compact(monkeypatch)
+
+    def no_dense(*args, **kw):  # no query of the chunk takes the dense decode path
+        raise AssertionError("an aligned-start chunk must not attend densely")
+
+    monkeypatch.setattr(ops, "attn_decode", no_dense)
+    # FlashPrefill: pooled scores over the partial blocks, the reference's rowwise rule
+    fp = dict(attention_sink=1, window_size=2, alpha=0.5, last_n_block=0, min_budget=3)
+    out, _ = flashprefill_compactattn_prefill_full_kv(
+        q.to(gpu), k.to(gpu), v.to(gpu), None, softmax_scale=SCALE, num_key_value_groups=G, block_size=64,
+        pack_impl="indexed_dense", indexed_impl="fi_zero_copy", cache_fill_backend="auto", **fp)
+    sc = oracle.block_scores(oracle.block_mean(bits(q)), oracle.block_mean(bits(k)), P, SCALE)
+    assert sc.shape[2:] == (Qb, cap)
+    table, counts = ref_flashprefill_tables(sc, P, Hkv, fp["alpha"], fp["attention_sink"], fp["window_size"],
+                                            fp["min_budget"], fp["last_n_block"])
+    gt, gc = (t.cpu().numpy() for t in calls[-1])
+    assert np.array_equal(gc, counts) and np.array_equal(gt, table)
+    check(out, table, counts)
+    # Seer: threshold on caller gate scores over ceil(q_len/64) x ceil(kv_len/64) blocks
+    logits = torch.randn((1, Hq, Qb, cap), generator=g) * 2.5
+    causal = torch.arange(cap)[None, :] <= (P[0] + torch.arange(Qb))[:, None]
+    gate = torch.softmax(logits.masked_fill(~causal, float("-inf")), dim=-1)
+    out, _ = chunked_prefill_column_dense_attention_forward(
+        q.to(gpu), k.to(gpu), v.to(gpu), None, q_len, softmax_scale=SCALE, attn_gate_score=gate.to(gpu),
+        threshold=0.05, num_key_value_groups=G, pack_impl="indexed_dense", indexed_impl="fi_zero_copy")
+    table, counts = ref_seer_tables(gate.numpy(), P, Hkv, 0.05, 2)
+    gt, gc = (t.cpu().numpy() for t in calls[-1])
+    assert np.array_equal(gc, counts) and np.array_equal(gt, table)
+    check(out, table, counts)
+    # caller keep masks over ceil(kv_len/64) blocks
+    keep_block = torch.rand((1, Hq, cap), generator=g) < 0.2
+    out, _ = chunked_prefill_column_dense_attention_from_keep_block(
+        q.to(gpu), k.to(gpu), v.to(gpu), keep_block.to(gpu), None, q_len, SCALE, num_key_value_groups=G)
+    kv = keep_block.view(1, Hkv, G, cap).any(dim=2).numpy().astype(np.uint8)
+    kv[..., P[0]:] = 1
+    table = np.full((Hkv, cap), -1, np.int32)
+    counts = np.zeros((Hkv,), np.int32)
+    for h in range(Hkv):
+        ids = np.nonzero(kv[0, h])[0]
+        table[h, :len(ids)] = ids
+        counts[h] = len(ids)
+    check(out, table, counts)
+
+
+@pytest.mark.parametrize("q_len", [1, 5, 64])
+def test_mid_block_and_single_token_calls_are_dense(gpu, q_len):
+    """q_len == 1 (FlashPrefill's dense fallback, flashprefill_prefill.py:903-907) and chunks of
+    at most 64 queries that start inside a block attend densely to all kv_len keys; a longer
+    chunk that starts inside a block raises."""
+    _print_case(test="mid_block_dense", q_len=q_len)
+    Hq, Hkv = 4, 2
+    kv_len = 64 * 9 + 20 + q_len  # the chunk starts 20 tokens into block 9
+    g = torch.Generator().manual_seed(100 + q_len)
     q = torch.randn((1, q_len, Hq, 128), generator=g).to(torch.bfloat16)
     k = torch.randn((1, kv_len, Hkv, 128), generator=g).to(torch.bfloat16)
     v = torch.randn((1, kv_len, Hkv, 128), generator=g).to(torch.bfloat16)
-    khf, vhf = k.transpose(1, 2).contiguous(), v.transpose(1, 2).contiguous()
+    ref = oracle.attention_decode(bits(q), bits(k.transpose(1, 2)), bits(v.transpose(1, 2)), [kv_len], SCALE)
+    fp = dict(attention_sink=1, window_size=2, alpha=0.3, last_n_block=0, min_budget=4, pack_impl="indexed_dense",
+              indexed_impl="fa2_paged", cache_fill_backend="auto")
+    out, stats = flashprefill_compactattn_prefill_full_kv(q.to(gpu), k.to(gpu), v.to(gpu), None, softmax_scale=SCALE,
+                                                          num_key_value_groups=2, block_size=64, **fp)
+    assert stats["flashprefill_dense_calls"] == 1.0
+    err = np.abs(f32(out) - ref)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
+    if q_len > 1:
+        gate = torch.rand((1, Hq, 2, -(-kv_len // 64)), generator=g)
+        out, _ = chunked_prefill_column_dense_attention_forward(
+            q.to(gpu), k.to(gpu), v.to(gpu), None, q_len, softmax_scale=SCALE, attn_gate_score=gate.to(gpu),
+            threshold=0.5, num_key_value_groups=2)
+        err = np.abs(f32(out) - ref)
+        assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN
+    long_q = torch.zeros((1, 65, Hq, 128), dtype=torch.bfloat16)
+    kk = torch.zeros((1, 64 * 3 + 10 + 65, Hkv, 128), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="block boundary"):
+        flashprefill_compactattn_prefill_full_kv(long_q.to(gpu), kk.to(gpu), kk.to(gpu), None, softmax_scale=SCALE,
+                                                 num_key_value_groups=2, block_size=64, **fp)
 
-    def check(out, table=None, counts=None):
-        got = f32(out)
-        if head:
-            ref = oracle.attention(bits(q[:, :head]), bits(khf[:, :, :past + head]), bits(vhf[:, :, :past + head]),
-                                   [past // 64], table, counts, SCALE)
-            err = np.abs(got[:, :head] - ref)
-            assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, ("head", err.max(), err.mean())
-        ref = oracle.attention_decode(bits(q[:, head:].contiguous()), bits(khf), bits(vhf), [kv_len], SCALE)
-        err = np.abs(got[:, head:] - ref)
-        assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, ("tail", err.max(), err.mean())
 
-    # FlashPrefill: the head's tables are the reference's rowwise selection over its keys
-    fp = dict(attention_sink=1, window_size=2, alpha=0.3, last_n_block=0, min_budget=4)
-    out, stats = flashprefill_compactattn_prefill_full_kv(
-        q.to(gpu), k.to(gpu), v.to(gpu), None, softmax_scale=SCALE, num_key_value_groups=G, block_size=64,
-        pack_impl="indexed_dense", indexed_impl="fi_zero_copy", cache_fill_backend="auto", **fp)
-    assert stats["flashprefill_dense_tail_tokens"] == q_len - head
-    table = counts = None
-    if head:
-        sc = oracle.block_scores(oracle.block_mean(bits(q[:, :head])), oracle.block_mean(bits(k[:, :past + head])),
-                                 [past // 64], SCALE)
-        table, counts = ref_flashprefill_tables(sc, [past // 64], Hkv, fp["alpha"], fp["attention_sink"],
-                                                fp["window_size"], fp["min_budget"], fp["last_n_block"])
-    check(out, table, counts)
-    if q_len < 2:
-        return  # the Seer entries require query_length > 1 (as the reference's)
-    # Seer: threshold on caller gate scores over the head's blocks
-    nqb, nkb = -(-q_len // 64), -(-kv_len // 64)
-    gate = torch.rand((1, Hq, nqb, nkb), generator=g) * 0.1
-    out, _ = chunked_prefill_column_dense_attention_forward(
-        q.to(gpu), k.to(gpu), v.to(gpu), None, q_len, softmax_scale=SCALE, attn_gate_score=gate.to(gpu),
-        threshold=0.08, num_key_value_groups=G, pack_impl="indexed_dense", indexed_impl="fi_zero_copy")
-    if head:
-        hg = gate[:, :, :head // 64, :(past + head) // 64].contiguous().numpy()
-        keep = oracle.select_rows(hg, [past // 64], oracle.Rule(threshold=0.08))
-        _, _, table, counts = oracle.union_compact(keep, Hkv, [past // 64])
-    check(out, table, counts)
-    keep_block = torch.rand((1, Hq, nkb), generator=g) < 0.3
-    out, _ = chunked_prefill_column_dense_attention_from_keep_block(
-        q.to(gpu), k.to(gpu), v.to(gpu), keep_block.to(gpu), None, q_len, SCALE, num_key_value_groups=G)
-    if head:
-        cap = (past + head) // 64
-        kv = keep_block[:, :, :cap].view(1, Hkv, G, cap).any(dim=2).numpy().astype(np.uint8)
-        kv[..., past // 64:] = 1
-        table = np.full((Hkv, cap), -1, np.int32)
-        counts = np.zeros((Hkv,), np.int32)
-        for h in range(Hkv):
-            ids = np.nonzero(kv[0, h])[0]
-            table[h, :len(ids)] = ids
-            counts[h] = len(ids)
-    check(out, table, counts)
+@pytest.mark.parametrize("q_len", [256, 256 + 64, 256 + 37])
+def test_flashprefill_entry_128_token_blocks(gpu, monkeypatch, q_len):
+    """block_size=128 (the reference's default, modeling_llama_flashprefill_compactattn.py:253):
+    128-token score blocks pooled from the 64-token means, the rowwise rule in 128-token block
+    units (a torch restatement of flashprefill_prefill.py:596-666 on the oracle's 128-token
+    scores), then both 64-token pages of every kept 128-token block (one when the chunk's last
+    128-token block has a single 64-token page).  Tables bit-exact; attention against the fp64
+    oracle; flash_prefill_compute_mean_k / score_chunked at block 128 agree with the oracle."""
+    _print_case(test="flashprefill_128", q_len=q_len)
+    Hq, Hkv, past = 8, 2, 64 * 40
+    G = Hq // Hkv
+    kv_len = past + q_len
+    cap64 = past // 64 + -(-q_len // 64)
+    g = torch.Generator().manual_seed(7 + q_len)
+    q = (torch.randn((1, q_len, Hq, 128), generator=g) + 3 * torch.randn((1, 1, Hq, 128), generator=g))
+    q = q.to(torch.bfloat16)
+    nb = -(-kv_len // 128)
+    offs = 2 * torch.randn((1, nb, 1, Hkv, 128), generator=g).expand(1, nb, 128, Hkv, 128).reshape(1, nb * 128, Hkv, 128)
+    k = (torch.randn((1, kv_len, Hkv, 128), generator=g) + offs[:, :kv_len]).to(torch.bfloat16)
+    v = torch.randn((1, kv_len, Hkv, 128), generator=g).to(torch.bfloat16)
+    calls = spy_union_compact(monkeypatch)
+    fp = dict(attention_sink=1, window_size=2, alpha=0.4, last_n_block=1, min_budget=3)
+    out, _ = flashprefill_compactattn_prefill_full_kv(
+        q.to(gpu), k.to(gpu), v.to(gpu), None, softmax_scale=SCALE, num_key_value_groups=G, block_size=128,
+        pack_impl="indexed_dense", indexed_impl="fa2_paged", cache_fill_backend="auto", **fp)
+    m64q, m64k = oracle.block_mean(bits(q)), oracle.block_mean(bits(k))
+    last = q_len - 64 * (m64q.shape[2] - 1)
+    q128 = oracle.pair_block_means(m64q, last)
+    k128 = oracle.pair_block_means(m64k, last)
+    P128 = [past // 128]
+    sc = oracle.block_scores(q128, k128, P128, SCALE)
+    t128, c128 = ref_flashprefill_tables(sc, P128, Hkv, fp["alpha"], fp["attention_sink"], fp["window_size"],
+                                         fp["min_budget"], fp["last_n_block"])
+    # the 128-token union is the one the entry built before naming pages
+    gt, gc = (t.cpu().numpy() for t in calls[-1])
+    assert np.array_equal(gc, c128) and np.array_equal(gt, t128)
+    table = np.full((Hkv, cap64), -1, np.int32)
+    counts = np.zeros((Hkv,), np.int32)
+    for r in range(Hkv):
+        pages = [p for kb in t128[r, :c128[r]] for p in (2 * kb, 2 * kb + 1) if p < cap64]
+        table[r, :len(pages)] = pages
+        counts[r] = len(pages)
+    assert (counts < cap64).any(), "the case should drop blocks"
+    ref = oracle.attention(bits(q), bits(_pad_keys(k, cap64)), bits(_pad_keys(v, cap64)), [past // 64], table, counts,
+                           SCALE)
+    err = np.abs(f32(out) - ref)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
+    # the vendor functions at block 128
+    mk = flash_prefill_compute_mean_k(k.to(gpu), block_size=128)
+    assert float_bits_equal(f32(mk.permute(0, 2, 1, 3)), k128)
+    scg = flash_prefill_score_chunked_from_mean_k(q.to(gpu), mk, key_len=kv_len, block_size=128)
+    assert float_bits_equal(f32(scg.permute(0, 3, 1, 2)), sc)
+    # a mean-K cache at block 128 gives the same output
+    out2, _ = flashprefill_compactattn_prefill_full_kv(
+        q.to(gpu), k.to(gpu), v.to(gpu), None, softmax_scale=SCALE, num_key_value_groups=G, block_size=128,
+        pack_impl="indexed_dense", indexed_impl="fa2_paged", cache_fill_backend="auto", mean_k_cache=mk, **fp)
+    assert torch.equal(out2, out)
 
 
 def test_flashprefill_first_chunk_is_dense(gpu):

@@ -90,6 +90,101 @@ def test_cache_fill_bit_exact(gpu, layout, gate):
             assert float_bits_equal(kg[b, :, past[b]:past[b] + qb], ref[b])
 
 
+@pytest.mark.parametrize("Lq", [37, 128 + 29])
+@pytest.mark.parametrize("layout", ["heads_first", "paged"])
+def test_partial_last_block(gpu, layout, Lq):
+    """A chunk whose length is not a multiple of 64 (ceil(Lq/64) blocks, the last holding
+    Lq % 64 tokens): the cache receives exactly its Lq rows (the rows past them keep their NaN
+    fill), the mean-K / query means / AttnGate pools of the partial block cover its valid
+    tokens (bit-exact against the oracle's restatement of compute_mean_vector and the ceil_mode
+    pools), and attention over tables that end in the partial block never reads past the
+    chunk (its NaN rows would poison the output) -- against the fp64 oracle."""
+    _print_case(test="partial_last_block", layout=layout, Lq=Lq)
+    B, Hkv, G, past = 2, 2, 3, [3, 7]
+    Hq = Hkv * G
+    qb = -(-Lq // 64)
+    cap = max(past) + qb
+    g = torch.Generator().manual_seed(Lq)
+    k_new = torch.randn((B, Lq, Hkv, 128), generator=g).to(torch.bfloat16)
+    v_new = torch.randn((B, Lq, Hkv, 128), generator=g).to(torch.bfloat16)
+    q = torch.randn((B, Lq, Hq, 128), generator=g).to(torch.bfloat16)
+    k_past = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16)
+    v_past = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16)
+    nan = float("nan")
+    if layout == "heads_first":
+        kc = torch.full((B, Hkv, cap * 64, 128), nan, dtype=torch.bfloat16)
+        vc = kc.clone()
+        for b in range(B):  # the past as it sits in the cache
+            kc[b, :, :64 * past[b]] = k_past[b, :, :64 * past[b]]
+            vc[b, :, :64 * past[b]] = v_past[b, :, :64 * past[b]]
+        kc, vc = kc.to(gpu), vc.to(gpu)
+        K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+    else:
+        rows = B * Hkv
+        pt = torch.randperm(rows * cap, generator=g).to(torch.int32).view(rows, cap).contiguous()
+        kc = torch.full((rows * cap, 64, 128), nan, dtype=torch.bfloat16)
+        vc = kc.clone()
+        for b in range(B):
+            for h in range(Hkv):
+                for kb in range(past[b]):
+                    kc[int(pt[b * Hkv + h, kb])] = k_past[b, h, 64 * kb:64 * kb + 64]
+                    vc[int(pt[b * Hkv + h, kb])] = v_past[b, h, 64 * kb:64 * kb + 64]
+        kc, vc, pt = kc.to(gpu), vc.to(gpu), pt.to(gpu)
+        K, V = ops.KV.paged(kc, pt), ops.KV.paged(vc, pt)
+    kmean = torch.full((B * Hkv, cap, 128), nan, device=gpu)
+    qhat = ops.cache_fill_pool_query(k_new.to(gpu), v_new.to(gpu), K, V, past, cap, kmean, q.to(gpu))
+    torch.cuda.synchronize()
+    # cache rows: the chunk's Lq rows at 64 * past[b], NaN after them
+    for b in range(B):
+        for h in range(Hkv):
+            if layout == "heads_first":
+                got_k = kc[b, h, 64 * past[b]:64 * (past[b] + qb)].cpu()
+            else:
+                got_k = torch.cat([kc[int(pt[b * Hkv + h, past[b] + j])].cpu() for j in range(qb)])
+            assert torch.equal(got_k[:Lq], k_new[b, :, h])
+            assert torch.isnan(got_k[Lq:].float()).all()
+    km = f32(kmean).reshape(B, Hkv, cap, 128)
+    means = oracle.block_mean(bits(k_new))
+    assert means.shape[2] == qb
+    for b in range(B):
+        assert float_bits_equal(km[b, :, past[b]:past[b] + qb], means[b])
+    assert float_bits_equal(f32(qhat), oracle.block_mean(bits(q)))
+    # AttnGate pools of the partial blocks (max, min, avg), projected per KV head and rotated
+    pools = ops.POOL_BITS["max"] | ops.POOL_BITS["min"] | ops.POOL_BITS["avg"]
+    wk = (torch.randn((Hkv, 3 * 128, 128), generator=g) * 0.02).float()
+    wq = (torch.randn((Hq, 128, 128), generator=g) * 0.02).float()
+    cos, sin = rope_tables(cap)
+    kgate = torch.full((B, Hkv, cap, 128), nan, device=gpu)
+    ops.gate_key_summaries(k_new.to(gpu), past, cap, pools, wk.to(gpu), kgate, rope_cos=cos.to(gpu),
+                           rope_sin=sin.to(gpu))
+    gq = ops.gate_query_summaries(q.to(gpu), past, cap, ops.POOL_BITS["avg"], wq.to(gpu), Hkv, rope_cos=cos.to(gpu),
+                                  rope_sin=sin.to(gpu))
+    ref_k = oracle.gate_project(oracle.block_pool(bits(k_new), pools), f32(wk), f32(cos), f32(sin), past)
+    ref_q = oracle.gate_project(oracle.block_mean(bits(q)), f32(wq), f32(cos), f32(sin), past)
+    kg = f32(kgate)
+    for b in range(B):
+        assert float_bits_equal(kg[b, :, past[b]:past[b] + qb], ref_k[b])
+    assert float_bits_equal(f32(gq), ref_q)
+    # attention over tables that end with the chunk's blocks (the partial one last)
+    kv_tab = torch.zeros((B, Hkv, cap), dtype=torch.uint8)
+    for b in range(B):
+        kv_tab[b, :, :past[b]] = (torch.rand((Hkv, past[b]), generator=g) < 0.5).to(torch.uint8)
+    table, counts = ops.compact_keep_kv(kv_tab.to(gpu), past, Lq, Hq, cap)
+    out, lse = ops.attn_fwd(q.to(gpu), K, V, table, counts, past, 128 ** -0.5, cap, Hkv, with_lse=True)
+    ktot = k_past.clone()
+    vtot = v_past.clone()
+    for b in range(B):
+        ktot[b, :, 64 * past[b]:64 * past[b] + Lq] = k_new[b].transpose(0, 1)
+        vtot[b, :, 64 * past[b]:64 * past[b] + Lq] = v_new[b].transpose(0, 1)
+    ref, ref_lse = oracle.attention(bits(q), bits(ktot), bits(vtot), past, table.cpu().numpy(), counts.cpu().numpy(),
+                                    128 ** -0.5, with_lse=True)
+    got = f32(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
+    assert np.abs(f32(lse) - ref_lse).max() <= 4e-3
+
+
 @pytest.mark.parametrize("layout", ["heads_first", "paged"])
 def test_cache_fill_pool_query_equals_separate_calls(gpu, layout):
     """The one-launch chunk summaries (cache append + mean-K + query-block means) against

@@ -260,26 +260,30 @@ SEER_GATES = {
 
 
 @pytest.mark.parametrize("selector", ["seer", "seer_keep_recent_7", "seer_kv_aware_gate", "seer_baseline",
-                                      "flashprefill"])
+                                      "flashprefill", "flashprefill_128", "seer_tail37", "flashprefill_tail37"])
 def test_layer_tables_bit_exact(gpu, selector):
     """Per layer, the tables the model builds for its last chunk equal the reference's
     selection recomputed from the layer's own inputs: for the Seer layer the restatement of the
     reference's rule (tests/util.ref_seer_tables) on the oracle's gate scores; for BASELINE's
-    sink + local variant and FlashPrefill the oracle's rule."""
+    sink + local variant and FlashPrefill the oracle's rule.  The _tail37 cases end the prompt
+    with a 37-token chunk, which selects with one partial query and key block."""
     print(f"case: model layer tables {selector}", flush=True)
     seer = selector.startswith("seer")
+    tlen = T + (37 if selector.endswith("_tail37") else 0)
     cls = SeerAttnLlamaChunkedDenseForCausalLM if seer else SeerAttnLlamaFlashPrefillCompactAttnForCausalLM
-    kw = dict(seerattn_compactattn_threshold=0.1)
+    kw = dict(seerattn_compactattn_threshold=0.1,
+              seerattn_flashprefill_block_size=128 if selector == "flashprefill_128" else 64)
     kw.update(SEER_GATES.get(selector, {}))
     m = _model(cls, gpu, qk_scale=8.0 if seer else 40.0, gate_scale=20.0, **kw)
     layer_idx = 1
     captured, handle, attn = _capture_layer_inputs(m, layer_idx)
-    ids = synthetic_prompt(1, T, m.config.vocab_size, 7, gpu)
+    ids = synthetic_prompt(1, tlen, m.config.vocab_size, 7, gpu)
     with torch.no_grad():
         run_chunked_prefill_once(m, ids, CHUNK)
     handle.remove()
     stats = attn._compactattn_last_stats
-    assert stats["past_blocks"] == (T - CHUNK) // 64
+    last_len = tlen - CHUNK * ((tlen - 1) // CHUNK)
+    assert stats["past_blocks"] == (tlen - last_len) // 64
     with torch.no_grad():
         parts = [_layer_qkv(attn, h, i * CHUNK, m) for i, h in enumerate(captured)]
     q_nope, k_nope, _, q_rope, _ = parts[-1]
@@ -303,12 +307,25 @@ def test_layer_tables_bit_exact(gpu, selector):
     else:
         qhat = oracle.block_mean(bits(q_rope))
         khat = oracle.block_mean(bits(k_rope_all))
-        scores = oracle.block_scores(qhat, khat, P, 1.0 / math.sqrt(128))
         rule = oracle.Rule(topk=c.seerattn_flashprefill_min_budget, alpha=c.seerattn_flashprefill_alpha,
                            sink_blocks=c.seerattn_flashprefill_attention_sink,
                            window_blocks=c.seerattn_flashprefill_window_size,
                            last_n_block=c.seerattn_flashprefill_last_n_block, topk_all_columns=True)
         last_n = c.seerattn_flashprefill_last_n_block
+        if selector == "flashprefill_128":  # 128-token score blocks, then both 64-token pages of each
+            P128 = [P[0] // 2]
+            scores = oracle.block_scores(oracle.pair_block_means(qhat, 64), oracle.pair_block_means(khat, 64), P128,
+                                         1.0 / math.sqrt(128))
+            _, _, t128, c128 = oracle.union_compact(oracle.select_rows(scores, P128, rule), Hkv, P128, last_n)
+            cap64 = P[0] + CHUNK // 64
+            table = np.full((Hkv, cap64), -1, np.int32)
+            counts = np.zeros((Hkv,), np.int32)
+            for r in range(Hkv):
+                pages = [2 * kb + i for kb in t128[r, :c128[r]] for i in (0, 1)]
+                table[r, :len(pages)] = pages
+                counts[r] = len(pages)
+        else:
+            scores = oracle.block_scores(qhat, khat, P, 1.0 / math.sqrt(128))
     if table is None:
         keep = oracle.select_rows(scores, P, rule)
         _, _, table, counts = oracle.union_compact(keep, Hkv, P, last_n)
@@ -316,19 +333,22 @@ def test_layer_tables_bit_exact(gpu, selector):
     got_table = stats["table"].cpu().numpy()
     assert np.array_equal(got_counts, counts)
     assert np.array_equal(got_table[:, :table.shape[1]], table)
-    nkb = P[0] + CHUNK // 64
+    nkb = P[0] + -(-last_len // 64)
     assert counts.min() < nkb, "the test wants a selective layer (some blocks dropped)"
     if selector == "seer_keep_recent_7":
         for r in range(Hkv):
             assert {P[0] - 3, P[0] - 2, P[0] - 1} <= set(table[r, :counts[r]].tolist())
-    # attention over the selected pages, recomputed from the layer's own inputs
+    # attention over the selected pages, recomputed from the layer's own inputs (the oracle's key
+    # arrays padded to whole blocks; a query never sees the padding)
     kc = k_rope_all.transpose(1, 2).contiguous()
     vc = v_all.transpose(1, 2).contiguous()
-    ref = oracle.attention(bits(q_rope), bits(kc), bits(vc), P, table, counts, 128 ** -0.5)
+    pad = (0, 0, 0, 64 * nkb - kc.shape[2])
+    ref = oracle.attention(bits(q_rope), bits(F.pad(kc, pad)), bits(F.pad(vc, pad)), P, table[:, :nkb], counts,
+                           128 ** -0.5)
     out = torch.empty_like(q_rope)
     from compactattention_amd import ops
     ops.attn_fwd(q_rope, ops.KV.heads_first(kc), ops.KV.heads_first(vc), stats["table"], stats["counts"], P,
-                 128 ** -0.5, kc.shape[2] // 64, Hkv, out=out)
+                 128 ** -0.5, nkb, Hkv, out=out)
     err = np.abs(f32(out) - ref)
     assert err.max() <= 2e-2 and err.mean() <= 2e-3, (err.max(), err.mean())
 

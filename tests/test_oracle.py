@@ -51,6 +51,56 @@ def test_block_mean_matches_fp64():
     assert np.abs(m - ref).max() <= 1e-6
 
 
+@pytest.mark.parametrize("L", [37, 64 * 3 + 5, 64 * 2 + 63])
+def test_block_mean_partial_last_block(L):
+    """A sequence of L tokens (not a multiple of 64) has ceil(L/64) blocks; the last averages
+    only its L % 64 tokens (compute_mean_vector's sum over the valid tokens / their count,
+    flashprefill_native_forward.py:78-88) -- an fp64 mean over those tokens; torch's
+    avg_pool3d with ceil_mode (AttnGate's pooling, attn_gate.py:113-130) agrees, and max /
+    min pooling covers those tokens only.  Whole blocks keep the 64-token mean bit for bit."""
+    x = _bf16((2, L, 3, 128))
+    nb = -(-L // 64)
+    r = L - 64 * (nb - 1)
+    m = oracle.block_mean(x)
+    assert m.shape == (2, 3, nb, 128)
+    xf = oracle.bf16_bits_to_f32(x).astype(np.float64)
+    ref_last = xf[:, 64 * (nb - 1):].mean(axis=1)  # [B, H, D]
+    assert np.abs(m[:, :, -1] - ref_last).max() <= 1e-6
+    if nb > 1:
+        assert float_bits_equal_np(m[:, :, :-1], oracle.block_mean(x[:, :64 * (nb - 1)]))
+    got = oracle.block_pool(x, oracle.pool_bits(("max", "avg")))
+    assert float_bits_equal_np(got[..., 128:], m)
+    assert np.array_equal(got[:, :, -1, :128], xf[:, 64 * (nb - 1):].max(axis=1).astype(np.float32))
+    if L >= 64:  # torch's pools refuse an input shorter than the kernel
+        t = torch.from_numpy(oracle.bf16_bits_to_f32(x)).double()
+        pooled = torch.nn.functional.avg_pool3d(t, kernel_size=[64, 1, 1], stride=[64, 1, 1], ceil_mode=True)
+        assert np.abs(m - pooled.numpy().transpose(0, 2, 1, 3)).max() <= 1e-6
+        mxp = torch.nn.functional.max_pool3d(t, kernel_size=[64, 1, 1], stride=[64, 1, 1], ceil_mode=True)
+        assert np.array_equal(got[..., :128], mxp.numpy().transpose(0, 2, 1, 3).astype(np.float32))
+    assert r < 64  # the case has a partial block
+
+
+@pytest.mark.parametrize("L", [128 * 3, 128 * 3 + 64, 128 * 2 + 37, 128 * 2 + 64 + 37, 100])
+def test_pair_block_means_are_128_token_means(L):
+    """128-token summaries from the 64-token means equal the fp64 mean of each 128-token block's
+    tokens (a partial last block's valid ones: compute_mean_vector at block_size 128,
+    flashprefill_native_forward.py:78-88); whole pairs equal (m0 + m1) / 2 bit for bit."""
+    x = _bf16((2, L, 3, 128))
+    m64 = oracle.block_mean(x)  # [B, H, ceil(L/64), D]
+    last = L - 64 * (m64.shape[2] - 1)
+    m128 = oracle.pair_block_means(m64, last)
+    nb = -(-L // 128)
+    assert m128.shape == (2, 3, nb, 128)
+    xf = oracle.bf16_bits_to_f32(x).astype(np.float64)
+    for j in range(nb):
+        ref = xf[:, 128 * j:min(L, 128 * j + 128)].mean(axis=1)
+        assert np.abs(m128[:, :, j] - ref).max() <= 2e-6, j
+    full = L // 128
+    if full:
+        half = ((m64[:, :, 0:2 * full:2] + m64[:, :, 1:2 * full:2]) * np.float32(0.5)).astype(np.float32)
+        assert float_bits_equal_np(m128[:, :, :full], half)
+
+
 def _rotate_half(x):
     x1, x2 = x[..., :64], x[..., 64:]
     return torch.cat((-x2, x1), dim=-1)

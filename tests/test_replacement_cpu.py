@@ -55,9 +55,12 @@ def test_replacement_structure(variant, cls):
 def test_replacement_argument_errors(tmp_path):
     with pytest.raises(ValueError, match="unsupported variant"):
         load_llama_attention_replacement_model(base_model=_stock(), variant="seer_block_sparse")
-    with pytest.raises(ValueError, match="64-token blocks"):
+    with pytest.raises(ValueError, match="64- or 128-token blocks"):
         load_llama_attention_replacement_model(base_model=_stock(), variant="flashprefill_compactattn",
-                                               flashprefill_block_size=128)
+                                               flashprefill_block_size=256)
+    # the reference's default FlashPrefill block (128 tokens) is the loader's default
+    fp = load_llama_attention_replacement_model(base_model=_stock(), variant="flashprefill_compactattn")
+    assert fp.compactattn_config.seerattn_flashprefill_block_size == 128
     r = load_llama_attention_replacement_model(base_model=_stock(), variant="seer_compactattn")
     with pytest.raises(ValueError, match="past_key_values"):
         r(input_ids=torch.randint(0, 512, (1, 64)), use_cache=False)
