@@ -286,6 +286,125 @@ def test_config3_layer_shape(gpu):
     _check_attention(ch.q, kc, vc, P, table, counts, cap, HKV, oracle_rows=((lq - 2, lq),))
 
 
+def test_config3_layer_attngate(gpu):
+    """One layer at config 3's shape with config 3's selector: the last 2048-token chunk of a
+    131072-token prompt (P = 2016 past blocks), 32 / 8 heads, AttnGate Qavg_Kavg with
+    force_double (per-head 128 x 128 projections of the pooled Q and K ~ N(0, 0.02), block
+    RoPE), softmax threshold 5e-3 + sink block + 2 local blocks.  Gate-K and gate-Q summaries,
+    per-row masks, tables and counts bit-exact against the oracle; every attention row against
+    the fp32 torch reference (the plan runs unsplit at this shape)."""
+    from compactattention_amd.synthetic import rope_tables
+
+    print("case: config 3 layer with AttnGate (chunk 2048 at the end of 131072 tokens, 32/8 heads)", flush=True)
+    lq = 2048
+    past = 131072 - lq
+    ch = make_chunk_device(past, lq, HQ, HKV, gpu, seed=78)
+    cap, P = ch.kv_cap, ch.past_blocks
+    g = torch.Generator().manual_seed(1234)
+    wq = (torch.randn((HQ, 128, 128), generator=g) * 0.02).float()
+    wk = (torch.randn((HKV, 128, 128), generator=g) * 0.02).float()
+    cos, sin = rope_tables(cap)
+    kc, vc = torch.zeros_like(ch.k), torch.zeros_like(ch.v)
+    K, V = ops.KV.heads_first(kc), ops.KV.heads_first(vc)
+    kmean = torch.zeros((HKV, cap, 128), dtype=torch.float32, device=gpu)
+    kgate = torch.zeros_like(kmean)
+    _fill(ch, K, V, kmean, past, lq, gate_wk=wk.to(gpu), rope_cos=cos.to(gpu), rope_sin=sin.to(gpu), kgate=kgate)
+    rule = ops.Rule(threshold=5e-3, sink_blocks=1, local_blocks=2)
+    qhat = ops.pool_query(ch.q, P, cap, gate_wq=wq.to(gpu), rope_cos=cos.to(gpu), rope_sin=sin.to(gpu))
+    rowmask, _ = ops.score_select(qhat, kgate, SCALE, rule, P, HKV, cap)
+    table, counts, _, _ = ops.union_compact(rowmask, P, HKV, cap)
+    torch.cuda.synchronize()
+    nkb = P[0] + lq // 64
+    means = oracle.block_mean(np.ascontiguousarray(bits(ch.k)[:, :, :nkb * 64].transpose(0, 2, 1, 3)))
+    khat = np.zeros((1, HKV, cap, 128), dtype=np.float32)
+    khat[:, :, :nkb] = oracle.gate_project(means, f32(wk), f32(cos), f32(sin), [0])
+    assert float_bits_equal(f32(kgate[:, :nkb]).reshape(1, HKV, nkb, 128), khat[:, :, :nkb])
+    qref = oracle.gate_project(oracle.block_mean(bits(ch.q)), f32(wq), f32(cos), f32(sin), P)
+    assert float_bits_equal(f32(qhat), qref)
+    keep = oracle.select_rows(oracle.block_scores(qref, khat, P, SCALE), P,
+                              oracle.Rule(threshold=5e-3, sink_blocks=1, local_blocks=2))
+    assert np.array_equal(unpack_rowmask(rowmask, cap), keep)
+    _, _, ref_tab, ref_cnt = oracle.union_compact(keep, HKV, P)
+    assert np.array_equal(counts.cpu().numpy(), ref_cnt)
+    assert np.array_equal(table.cpu().numpy(), ref_tab)
+    assert ref_cnt.min() < nkb
+    _check_attention(ch.q, kc, vc, P, table, counts, cap, HKV, oracle_rows=((lq - 2, lq),))
+
+
+def test_config3_full_width_model(gpu):
+    """Config 3's decoder at full width with two of its 32 layers: hidden 4096, 32 / 8 heads,
+    SwiGLU 14336, vocab 128256, RoPE theta 5e5, random N(0, 0.02) bf16 weights, AttnGate
+    Qavg_Kavg with force_double + threshold 5e-3 + sink + 2 local blocks at both layers; an
+    8192-token prompt in 2048-token chunks (the first dense).  For each layer and each selecting
+    chunk the tables the model built equal the oracle's, recomputed from the hidden states the
+    layer received (gate pooling, projection, RoPE, scores, masks, unions), and the last
+    chunk's attention rows match the fp32 torch reference over the layer's own K/V."""
+    from compactattention_amd.chunked_prefill import synthetic_prompt
+    from compactattention_amd.prefill_sparse.llama import SeerAttnLlamaChunkedDenseForCausalLM, SeerAttnLlamaConfig
+    from compactattention_amd.prefill_sparse.llama.modeling_llama_common import apply_rotary_pos_emb, project_qkv
+    from compactattention_amd.synthetic import BASELINE_SEER
+
+    from .util import oracle_gate_summaries
+
+    print("case: config 3 full-width model (2 layers, hidden 4096, 8192-token prompt, chunk 2048)", flush=True)
+    tokens, chunk = 8192, 2048
+    cfg = SeerAttnLlamaConfig(num_hidden_layers=2, max_position_embeddings=tokens, **BASELINE_SEER)
+    model = SeerAttnLlamaChunkedDenseForCausalLM(cfg, device=gpu)
+    model.init_weights(seed=1234)
+    ids = synthetic_prompt(1, tokens, cfg.vocab_size, 1234 + 131072 * 104729, gpu)
+    captured = {i: [] for i in range(2)}
+    sinks = {}
+    hooks = []
+    for i, layer in enumerate(model.model.layers):
+        attn = layer.self_attn
+        attn.table_sink = sinks.setdefault(i, [])
+        attn.compactattn_debug = True
+        hooks.append(attn.register_forward_pre_hook(
+            lambda mod, args, i=i: captured[i].append(args[0].detach().clone())))
+    cache = model.new_cache(1, tokens)
+    with torch.no_grad():
+        for s0 in range(0, tokens, chunk):
+            model(ids[:, s0:s0 + chunk], cache)
+            # the tables of this chunk, per layer (the debug stats hold the last call's)
+            for i, layer in enumerate(model.model.layers):
+                st = layer.self_attn._compactattn_last_stats
+                sinks[i][-1] = (st["table"].clone(), st["counts"].clone(), st["past_blocks"])
+    for h in hooks:
+        h.remove()
+    bcos, bsin = (f32(t) for t in model.model.rotary_emb.blocks())
+    rule = oracle.Rule(threshold=5e-3, sink_blocks=1, local_blocks=2)
+    Hkv = cfg.num_key_value_heads
+    for i, layer in enumerate(model.model.layers):
+        attn = layer.self_attn
+        with torch.no_grad():
+            parts = [project_qkv(attn, h) for h in captured[i]]
+        k_nope_all = torch.cat([p[1] for p in parts], dim=1)
+        for c in range(1, tokens // chunk):  # chunk 0 is dense
+            table, counts, past = sinks[i][c]
+            P = [past]
+            assert past == c * chunk // 64
+            qhat, khat = oracle_gate_summaries(attn.attn_gate, bits(parts[c][0]), bits(k_nope_all[:, :(c + 1) * chunk]),
+                                               bcos, bsin, P[0])
+            keep = oracle.select_rows(oracle.block_scores(qhat, khat, P, 128 ** -0.5), P, rule)
+            _, _, ref_tab, ref_cnt = oracle.union_compact(keep, Hkv, P)
+            assert np.array_equal(counts.cpu().numpy(), ref_cnt), (i, c)
+            assert np.array_equal(table.cpu().numpy()[:, :ref_tab.shape[1]], ref_tab), (i, c)
+        # the last chunk's attention over the layer's own RoPE'd K/V
+        cos, sin = model.model.rotary_emb.tokens(0, tokens)
+        with torch.no_grad():
+            q_last = parts[-1][0]
+            k_all = torch.cat([p[1] for p in parts], dim=1)
+            v_all = torch.cat([p[2] for p in parts], dim=1)
+            qr, _ = apply_rotary_pos_emb(q_last, q_last, cos[-chunk:], sin[-chunk:])
+            _, kr = apply_rotary_pos_emb(k_all, k_all, cos, sin)
+        kc = kr.transpose(1, 2).contiguous()
+        vc = v_all.transpose(1, 2).contiguous()
+        table, counts, past = sinks[i][-1]
+        out = ops.attn_fwd(qr.contiguous(), ops.KV.heads_first(kc), ops.KV.heads_first(vc), table, counts, [past],
+                           SCALE, tokens // 64, Hkv)
+        torch_reference_check(out, qr.contiguous(), kc, vc, [past], table, counts, SCALE)
+
+
 # ----------------------------------------------------------------------------- config 4
 def test_fullsize_config4_ragged(gpu):
     """Config 4: four requests with cached pasts 16384 / 49152 / 98304 / 131072 tokens, a
