@@ -253,9 +253,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     const int n = l & 31;
 
     // ---- Q fragments (B operand of S^T = K Q^T) ----
-    // Q is scaled by softmax scale * log2(e) once (fp32, rounded back to bf16), so the score
-    // MFMAs produce log2-domain logits and the softmax needs no per-element scaling.
-    const float sl2 = p.scale_log2;
     const int qrow = r0 + 32 * w + n;
     const bool qvalid = qrow < rows_total;
     const int qt = qvalid ? qrow / G : 0;
@@ -266,8 +263,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
 #pragma unroll
         for (int ds = 0; ds < 8; ++ds) {
             if (qvalid) {
-                const f32x8_t x = __builtin_convertvector(*reinterpret_cast<const bf16x8_t*>(qp + 16 * ds), f32x8_t);
-                qf[ds] = __builtin_convertvector(x * sl2, bf16x8_t);
+                qf[ds] = *reinterpret_cast<const bf16x8_t*>(qp + 16 * ds);
             } else {
                 u32x4_t z = {0u, 0u, 0u, 0u};
                 qf[ds] = __builtin_bit_cast(bf16x8_t, z);
@@ -283,11 +279,6 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         for (int j = 0; j < 16; ++j) oacc[dt][j] = 0.0f;
     float m_run = -__builtin_inff();
     float l_run = 0.0f;
-    // the score accumulators start at -m_base (m_base = m_run, or 0 before the row's first key),
-    // so the S^T MFMAs yield s - m_base and the exponentials take them as they are
-    f32x16_t negm;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) negm[j] = 0.0f;
 
     const uint16_t* kbase_row = p.k.data + b * p.k.sb + hk * p.k.sh;
     const uint16_t* vbase_row = p.v.data + b * p.v.sb + hk * p.v.sh;
@@ -335,9 +326,11 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         }
     };
 
-    // One 64-key block: S^T = K Q^T - m_base (16 MFMAs), online softmax with lazy rescale, then
-    // O^T += V^T P^T (16 MFMAs).  m_run only rises when a row's block max exceeds it by more
-    // than kRescale (log2 units); otherwise P = exp2(s - m_run) < 2^kRescale and the
+    const float sl2 = p.scale_log2;
+
+    // One 64-key block: S^T = K Q^T (16 MFMAs), online softmax with lazy rescale, then
+    // O^T += V^T P^T (16 MFMAs).  m_run only rises when a row's scaled block max exceeds it
+    // by more than kRescale (log2 units); otherwise P = exp2(s - m_run) < 2^kRescale and the
     // accumulators keep their scale.
     // Fragment addresses.  K (A operand of S^T): lane row swap23(n) (+32 per 32-key half),
     // 16 bytes at d = 16 ds + 8 h.  V^T (A operand of O^T): each transposed b64 read gives
@@ -357,9 +350,12 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
         const uint8_t* ks = stage_base;
         const uint8_t* vs = stage_base + kKBytes;
         f32x16_t sacc[2];
-        // the two 32-key accumulators alternate so consecutive MFMAs are independent (the first
-        // of each chain reads -m_base as its accumulator input); the K fragment reads run six
-        // ahead of the MFMAs (scheduling groups below)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) sacc[kt][j] = 0.0f;
+        // the two 32-key accumulators alternate so consecutive MFMAs are independent; the
+        // K fragment reads run six ahead of the MFMAs (scheduling groups below)
         __builtin_amdgcn_s_setprio(1);
         {
             bf16x8_t kfr[16];
@@ -367,8 +363,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
             for (int i = 0; i < 16; ++i) kfr[i] = *reinterpret_cast<const bf16x8_t*>(ks + k_off[i >> 1] + (i & 1) * 8192);
 #pragma unroll
             for (int i = 0; i < 16; ++i)
-                sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[i], qf[i >> 1], i < 2 ? negm : sacc[i & 1],
-                                                                      0, 0, 0);
+                sacc[i & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kfr[i], qf[i >> 1], sacc[i & 1], 0, 0, 0);
             __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // 6 LDS reads
 #pragma unroll
             for (int i = 0; i < 10; ++i) {
@@ -390,32 +385,25 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
                     if (key > vis) sacc[kt][j] = -__builtin_inff();
                 }
         }
-        // the row's block max relative to m_base
         float mx = -__builtin_inff();
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
             for (int j = 0; j < 16; ++j) mx = fmaxf(mx, sacc[kt][j]);
-        mx = xor32_max(mx);
-        const bool first = m_run == -__builtin_inff();
-        const bool grow = first ? mx != -__builtin_inff() : mx > kRescale;
-        if (__ballot(grow)) {  // a row's first keys, or a max beyond the slack: rare
-            const float delta = grow ? mx : 0.0f;
-            const float alpha = grow ? (first ? 0.0f : __builtin_amdgcn_exp2f(-mx)) : 1.0f;
-            m_run = grow ? (first ? mx : m_run + mx) : m_run;
+        mx = xor32_max(mx) * sl2;
+        float alpha = 1.0f;
+        if (mx > m_run + kRescale) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mx);  // 0 when m_run = -inf
+            m_run = mx;
             l_run *= alpha;
+        }
+        if (__ballot(alpha != 1.0f)) {
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
                 for (int j = 0; j < 16; ++j) oacc[dt][j] *= alpha;
-#pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-                for (int j = 0; j < 16; ++j) sacc[kt][j] -= delta;
-            const float nb = m_run == -__builtin_inff() ? 0.0f : -m_run;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) negm[j] = nb;
         }
+        const float m_use = m_run == -__builtin_inff() ? 0.0f : m_run;
         bf16x8_t pf[4];
         float rs = 0.0f;
         const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
@@ -424,7 +412,7 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
             f32x8_t pv8;
 #pragma unroll
             for (int i = 0; i < 8; ++i)
-                pv8[i] = __builtin_amdgcn_exp2f(sacc[s4 >> 1][8 * (s4 & 1) + i]);
+                pv8[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[s4 >> 1][8 * (s4 & 1) + i], sl2, -m_use));
             pf[s4] = __builtin_convertvector(pv8, bf16x8_t);
             // the normaliser sums the bf16-rounded weights the PV product uses
             rs = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[s4], pf[s4], 0, 1), ones, rs, false);
@@ -735,11 +723,6 @@ __global__ __launch_bounds__(kDecWaves * 64) void attn_decode_kernel(AttnParams 
     for (int dt = 0; dt < 8; ++dt) oacc[dt] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -__builtin_inff();
     float l_run = 0.0f;
-    // the score accumulators start at -m_base (m_base = m_run, or 0 before the row's first key),
-    // so the S^T MFMAs yield s - m_base and the exponentials take them as they are
-    f32x16_t negm;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) negm[j] = 0.0f;
     const bf16x2_t ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
 
     auto compute = [&](int st, int set) {

@@ -625,6 +625,43 @@ def test_attention_ragged_unsplit_choice(gpu, even):
     assert err.max().item() <= ATOL_MAX and err.mean().item() <= ATOL_MEAN
 
 
+@pytest.mark.parametrize("splits", [1, 2])
+def test_attention_large_logits(gpu, splits):
+    """Scores up to ~45 in log2 units (a shared direction in every query of a head and an
+    offset per key block, as long-context models show): the softmax must take the scale
+    in fp32 on the MFMA's fp32 scores.  Rounding q * scale * log2(e) to bf16 before the
+    product instead gives each score a relative error of 2^-9, which at these magnitudes
+    moves the output by ~3e-2, past the tolerance."""
+    _print_case(test="attention_large_logits", splits=splits)
+    B, Hq, Hkv, Lq, P = 1, 8, 2, 256, 40
+    cap = P + Lq // 64
+    g = torch.Generator().manual_seed(57)
+    q = (torch.randn((B, Lq, Hq, 128), generator=g) + 3 * torch.randn((B, 1, Hq, 128), generator=g))
+    offs = 2 * torch.randn((B, Hkv, cap, 1, 128), generator=g).expand(B, Hkv, cap, 64, 128)
+    k = torch.randn((B, Hkv, cap * 64, 128), generator=g) + offs.reshape(B, Hkv, cap * 64, 128)
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    v = torch.randn((B, Hkv, cap * 64, 128), generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(128)
+    s = (q.double()[0, :, 0] @ k.double()[0, 0].T) * scale * math.log2(math.e)
+    assert s.abs().max() > 30  # the regime this test is for
+    keep_kv = (torch.rand((B, Hkv, cap), generator=g) < 0.5).to(torch.uint8)
+    table, counts = ops.compact_keep_kv(keep_kv.to(gpu), [P], Lq, Hq, cap)
+    K, V = ops.KV.heads_first(k.to(gpu)), ops.KV.heads_first(v.to(gpu))
+    out = ops.attn_fwd(q.to(gpu), K, V, table, counts, [P], scale, cap, Hkv, num_splits=splits)
+    torch.cuda.synchronize()
+    ref = oracle.attention(bits(q), bits(k), bits(v), [P], table.cpu().numpy(), counts.cpu().numpy(), scale)
+    err = np.abs(f32(out) - ref)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
+    # the decode kernel on the same inputs: the chunk's last 5 rows over the whole cache
+    kv_len = [cap * 64]
+    q5 = q[:, -5:].contiguous()
+    dec = ops.attn_decode(q5.to(gpu), K, V, kv_len, scale, cap, Hkv, num_splits=splits)
+    torch.cuda.synchronize()
+    dref = oracle.attention_decode(bits(q5), bits(k), bits(v), kv_len, scale)
+    err = np.abs(f32(dec) - dref)
+    assert err.max() <= ATOL_MAX and err.mean() <= ATOL_MEAN, (err.max(), err.mean())
+
+
 def test_attention_all_selected_equals_dense(gpu):
     """Keeping every block reduces to dense causal attention (checked against torch fp32 SDPA)."""
     _print_case(test="attention_dense")
