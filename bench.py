@@ -265,6 +265,9 @@ def main() -> int:
                                   "tflops": round(fl / (a_us * 1e-6) / 1e12, 1),
                                   "speedup_vs_dense": round(dense_us / a_us, 3)}
 
+    paged = paged_pool_line(dev, q, k_new, v_new, kc, vc, P, cap, HKV, rule, splits, table, counts, flops,
+                            args.steps, timed, graph_timed)
+
     # algorithmic HBM bytes of the memory-bound stages
     hbm_bytes = {
         "cache_fill": 2 * LQ * HKV * 128 * 2 * 2 + QB * HKV * 128 * 4,
@@ -309,6 +312,7 @@ def main() -> int:
         "stage_us_eager": {k: round(v, 2) for k, v in stage_us_eager.items()},
         "stage_hbm_frac": hbm_frac,
         "sweep": sweep,
+        "paged_pool": paged,
         "roofline": {
             "bound": "mfma",
             "achieved": round(attn_tflops, 2),
@@ -346,6 +350,79 @@ def main() -> int:
 
     print(json.dumps(result), flush=True)
     return 0
+
+
+def paged_pool_line(dev, q, k_new, v_new, kc, vc, P, cap, hkv, rule, splits, table, counts, flops, steps, timed,
+                    graph_timed):
+    """Config 2 with the cache in a global page pool read through a permuted page table (every
+    logical block of every KV row on a random physical page), the same step and inputs as the
+    heads-first value: its per-chunk time, graph-replayed path and attention, and whether its
+    output equals the heads-first cache's bit for bit."""
+    import torch
+
+    from compactattention_amd import ops
+
+    progress("paged-pool cache with a permuted page table")
+    scale = 1.0 / math.sqrt(128)
+    rows = hkv
+    pages = rows * cap
+    gen = torch.Generator(device="cpu").manual_seed(4321)
+    perm = torch.randperm(pages, generator=gen).to(torch.int32)
+    pt = perm.view(rows, cap).to(dev)
+    kpool = torch.zeros((pages, 64, 128), dtype=torch.bfloat16, device=dev)
+    vpool = torch.zeros_like(kpool)
+    KP, VP = ops.KV.paged(kpool, pt), ops.KV.paged(vpool, pt)
+    # copy the past (what the heads-first cache holds) page by page into the pool
+    idx = pt[:, :P[0]].long().reshape(-1)
+    kpool[idx] = kc[0, :, :P[0] * 64].reshape(rows * P[0], 64, 128)
+    vpool[idx] = vc[0, :, :P[0] * 64].reshape(rows * P[0], 64, 128)
+    kmean_p = torch.zeros((hkv, cap, 128), dtype=torch.float32, device=dev)
+    for t0 in range(0, P[0] * 64, 16384):
+        t1 = min(P[0] * 64, t0 + 16384)
+        ops.cache_fill(kc[0:1, :, t0:t1].transpose(1, 2).contiguous(), None, None, None, [t0 // 64], cap, kmean_p)
+    ws = torch.empty((max(ops.attn_workspace_bytes(P, q.shape[1], q.shape[2], hkv, cap, splits), 16),),
+                     dtype=torch.uint8, device=dev)
+    out_p = torch.empty_like(q)
+
+    def step():
+        qhat = ops.cache_fill_pool_query(k_new, v_new, KP, VP, P, cap, kmean_p, q)
+        rowmask, _ = ops.score_select(qhat, kmean_p, scale, rule, P, hkv, cap)
+        tb, ct, _, _ = ops.union_compact(rowmask, P, hkv, cap)
+        ops.attn_fwd(q, KP, VP, tb, ct, P, scale, cap, hkv, out=out_p, num_splits=splits, workspace=ws)
+        return tb, ct
+
+    for _ in range(5):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / steps * 1e6
+    tb, ct = step()
+    torch.cuda.synchronize()
+    same_tables = bool(torch.equal(tb, table) and torch.equal(ct, counts))
+    out_hf = torch.empty_like(q)  # the heads-first cache through the same tables
+    ops.attn_fwd(q, ops.KV.heads_first(kc), ops.KV.heads_first(vc), tb, ct, P, scale, cap, hkv, out=out_hf,
+                 num_splits=splits, workspace=ws)
+    torch.cuda.synchronize()
+    same_out = bool(torch.equal(out_p.view(torch.int16), out_hf.view(torch.int16)))
+    attn = lambda: ops.attn_fwd(q, KP, VP, tb, ct, P, scale, cap, hkv, out=out_p, num_splits=splits, workspace=ws)
+    attn_us = timed(attn)
+    line = {
+        "workload": "config 2 with K/V in a global page pool [pages, 64, 128] read through a page table whose "
+                    "entries are a random permutation of the pool (same inputs, rule and step as `value`)",
+        "us_per_chunk": round(us, 2),
+        "path_us_graph": round(graph_timed(step, reps=5, replays=4), 2),
+        "attn_us": round(attn_us, 2),
+        "attn_us_graph": round(graph_timed(attn, reps=5, replays=4), 2),
+        "attn_tflops": round(flops / (attn_us * 1e-6) / 1e12, 1),
+        "tables_equal_heads_first": same_tables,
+        "output_equal_heads_first": same_out,
+    }
+    del kpool, vpool, KP, VP, ws
+    torch.cuda.empty_cache()
+    return line
 
 
 def shard_share(dev, past: int, chunk: int, hq: int, hkv: int, keep: float, steps: int = 20):
@@ -738,22 +815,25 @@ def model_prefill(tokens, chunk, layers, dev, seer_only: bool = False):
     progress(f"model prefill: FlashPrefill at {fp['keep_ratio_last_chunk']:.3f} keep {fp['seconds']:.2f} s")
     del fmodel, fcache
     torch.cuda.empty_cache()
+    keep_pct = 100.0 * seer["keep_ratio_last_chunk"]
     out = {
         "workload": f"config 3: Llama-3.1-8B-shaped decoder ({layers} layers, hidden 4096, 32 Q / 8 KV heads, "
                     f"SwiGLU 14336, vocab 128256), random N(0,0.02) bf16 weights, {tokens}-token synthetic prompt, "
-                    f"chunk {chunk}, AttnGate Qavg_Kavg + threshold 5e-3 + sink + 2 local blocks at every layer, "
-                    "first chunk dense, logits of the last token only",
+                    f"chunk {chunk}, first chunk dense, logits of the last token only; three selectors on the same "
+                    "decoder weights",
         "linear_flop": linear_flops,
-        "linear_tflops_per_s": round(linear_flops / seer["seconds"] / 1e12, 1),
-        "dense_tok_per_s": dense["tok_per_s"], "dense_seconds": dense["seconds"],
-        "dense_attention_share": dense["attention_share"], "dense_roofline": dense["roofline"],
-        "speedup_vs_dense": round(dense["seconds"] / seer["seconds"], 3),
         "flashprefill_quarter": dict(fp, speedup_vs_dense=round(dense["seconds"] / fp["seconds"], 3),
                                      selector="FlashPrefill pooled scores, min_budget top-k over all columns "
                                               "(calibrated to ~25 % of the last chunk's past), alpha 1.0, sink 2, "
-                                              "window 4"),
+                                              "window 4: the sparse-attention line"),
+        "seer_attngate": dict(seer, speedup_vs_dense=round(dense["seconds"] / seer["seconds"], 3),
+                              linear_tflops_per_s=round(linear_flops / seer["seconds"] / 1e12, 1),
+                              selector="AttnGate Qavg_Kavg + force_double, threshold 5e-3 + sink + 2 local blocks "
+                                       "(BASELINE config 3's rule) at every layer",
+                              label=f"random gates keep {keep_pct:.2f} % of the past (last chunk): attention is "
+                                    "almost only the chunk's own blocks, so this line is bound by the linear layers"),
+        "dense": dict(dense, selector="every chunk dense (identity tables)"),
     }
-    out.update(seer)
     return out
 
 
