@@ -76,6 +76,11 @@ struct AttnParams {
     // row's selected count is within 1.5x of their mean (workgroup 0 records the choice
     // here for the merge); null otherwise
     int32_t* ws_unsplit;
+    // K and V without page tables, 64-token blocks contiguous in token order (stride_blk =
+    // 64 stride_tok) and every request's tokens within 2^31 bytes: the DMA addresses a block
+    // through one buffer resource per KV row (the block's byte offset in the scalar offset),
+    // whose range ends at the request's last token as the per-block resources do
+    int row_res;
     int32_t qpos0[CA_MAX_BATCH];     // absolute position of each request's query row 0
     int32_t nkb[CA_MAX_BATCH];       // valid logical blocks of each request
     int32_t sp[CA_MAX_BATCH];        // splits of each request's block lists
@@ -308,8 +313,28 @@ __global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2))) vo
     // and 0 * V must not meet a non-finite V).  Row offsets go in the VGPR offset, which the
     // range check covers.
     const int kv_tokens = qpos0 + s.Lq;
+    const __amdgpu_buffer_rsrc_t rk_row =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase_row), 0, kv_tokens * kstok_b, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv_row =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase_row), 0, kv_tokens * vstok_b, 0x00020000);
+    const int kblk_b = 64 * kstok_b;
+    const int vblk_b = 64 * vstok_b;
     auto issue_block = [&](int e, int stage) {
         const int kb = block_id(e);
+        if (p.row_res) {
+            uint8_t* kdst = smem + stage * kStageBytes + wu * 1024;
+            uint8_t* vdst = kdst + kKBytes;
+            // the block offset goes in the vector offset, which the range check covers (the
+            // scalar offset is not checked)
+            const int ko = k_goff + kb * kblk_b;
+            const int vo = v_goff + kb * vblk_b;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rk_row, to_lds(kdst + i * 8192), 16, ko + i * 32 * kstok_b, 0, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rv_row, to_lds(vdst + i * 8192), 16, vo + i * 32 * vstok_b, 0, 0, 0);
+            }
+            return;
+        }
         const int64_t kphys = kpt ? clamp_page(sload(kpt + kb), p.k.max_page) : kb;
         const int64_t vphys = vpt ? clamp_page(sload(vpt + kb), p.v.max_page) : kb;
         const int rows = min(kv_tokens - kb * 64, 64);
@@ -1076,6 +1101,13 @@ hipError_t launch_attn(const AttnArgs& a, hipStream_t stream) {
     p.ws_unsplit = plan.max > 1 && plan.may_unsplit && a.table
                        ? reinterpret_cast<int32_t*>(p.ws_lse + (int64_t)plan.max * rows_all)
                        : nullptr;
+    {
+        int max_tokens = 0;
+        for (int b = 0; b < a.s.B; ++b) max_tokens = max(max_tokens, p.qpos0[b] + a.s.Lq);
+        const int64_t stok = max(a.k.stok, a.v.stok);
+        p.row_res = a.k.page_table == nullptr && a.v.page_table == nullptr && a.k.sblk == 64 * a.k.stok &&
+                    a.v.sblk == 64 * a.v.stok && (int64_t)max_tokens * stok * 2 + 64 * stok * 2 < (int64_t{1} << 31);
+    }
     if (a.table)
         hipLaunchKernelGGL((attn_fwd_kernel<kNW, true>), dim3(p.per_xcd * 8), dim3(kNW * 64), 0, stream, p);
     else if (attn_uses_decode_kernel(a.s, true))
