@@ -223,6 +223,8 @@ def main() -> int:
         "pool_query": lambda: ops.pool_query(q, P, cap),
         "score_select": lambda: ops.score_select(qhat, kmean, scale, rule, P, HKV, cap),
         "union_compact": lambda: ops.union_compact(rowmask, P, HKV, cap),
+        # the reference's per-token FlashPrefill scores (an optional score form; not in the step)
+        "token_mass_scores": lambda: ops.score_token_mass(q, kmean, scale, P, HKV, cap, 64),
         "attention": lambda: ops.attn_fwd(q, K, V, table, counts, P, scale, cap, HKV, out=out, num_splits=splits,
                                           workspace=ws),
     }

@@ -46,6 +46,7 @@ EXPORTED = (
     "ca_gate_query_summaries",
     "ca_pair_block_summaries",
     "ca_score_select",
+    "ca_score_token_mass",
     "ca_select_scores",
     "ca_union_compact",
     "ca_compact_keep_kv",
@@ -136,6 +137,7 @@ _SIGNATURES = {
                                                _vp, _vp]),
     "ca_pair_block_summaries": (ctypes.c_int, [_vp, _i64, _vp, _i64, _i64, _i32, _i32, _vp]),
     "ca_score_select": (ctypes.c_int, [_P(Dims), _vp, _vp, _f32, _P(SelectRule), _vp, _vp, _vp, _vp]),
+    "ca_score_token_mass": (ctypes.c_int, [_P(Dims), _P(SeqLayout), _vp, _i64, _i32, _f32, _vp, _vp, _vp]),
     "ca_select_scores": (ctypes.c_int, [_P(Dims), _vp, _i32, _i64, _i64, _i64, _P(SelectRule), _vp, _vp, _vp]),
     "ca_union_compact": (ctypes.c_int, [_P(Dims), _vp, _i32, _vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "ca_compact_keep_kv": (ctypes.c_int, [_P(Dims), _vp, _vp, _vp, _i64, _vp, _vp]),

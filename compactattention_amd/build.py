@@ -17,7 +17,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB_NAME = "libcompactattn_hip.so"
 LIB_PATH = os.path.join(HERE, LIB_NAME)
-SOURCES = ["ca_api.hip", "ca_select.hip", "ca_attn.hip", "ca_model.hip"]
+SOURCES = ["ca_api.hip", "ca_select.hip", "ca_score_token.hip", "ca_attn.hip", "ca_model.hip"]
 HEADERS = ["ca_common.h", "ca_kernels.h"]
 
 

@@ -400,6 +400,37 @@ int ca_score_select(const ca_dims* dims, const float* qhat, const float* khat, f
     return ok();
 }
 
+int ca_score_token_mass(const ca_dims* dims, const ca_seq_layout* q, const float* khat, int64_t khat_stride,
+                        int32_t block_size, float scale, const int32_t* past_blocks_host, float* scores,
+                        void* stream) {
+    if (dims == nullptr || past_blocks_host == nullptr) return fail(CA_ERR_INVALID, "dims and past_blocks are required");
+    if (block_size != 64 && block_size != 128) return fail(CA_ERR_INVALID, "block_size=%d (64 or 128)", block_size);
+    // dims count block_size blocks: the 64-token shape checks run on the same numbers with the
+    // chunk's blocks counted in block_size units
+    ca_dims d64 = *dims;
+    const int qb = (dims->q_len + block_size - 1) / block_size;
+    d64.q_len = qb * CA_BLOCK;  // Qb = qb in the shape checks below
+    ca::Shape s;
+    ca::PastBlocks pb;
+    int max_nkb = 0, rc;
+    if ((rc = check_dims(&d64, past_blocks_host, &s, &pb, &max_nkb)) != CA_OK) return rc;
+    s.Lq = dims->q_len;
+    ca::SeqAddr qa;
+    if ((rc = check_seq(q, "q", &qa)) != CA_OK) return rc;
+    if (khat == nullptr || scores == nullptr) return fail(CA_ERR_INVALID, "khat and scores are required");
+    if (!aligned16(khat) || !aligned16(scores)) return fail(CA_ERR_INVALID, "khat and scores must be 16-byte aligned");
+    if (khat_stride < max_nkb)
+        return fail(CA_ERR_INVALID, "khat_stride=%lld < key blocks per row %d", (long long)khat_stride, max_nkb);
+    for (int b = 0; b < s.B; ++b)
+        if ((int64_t)past_blocks_host[b] * block_size > ((int64_t)1 << 30))
+            return fail(CA_ERR_LIMIT, "past_blocks[%d]=%d: positions beyond 2^30 tokens", b, past_blocks_host[b]);
+    if (ca::token_mass_lds_bytes(s) > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap=%d too large", s.cap);
+    hipError_t e = ca::launch_token_mass(s, qa, khat, khat_stride, block_size, scale, pb, scores,
+                                         static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "score_token_mass launch");
+    return ok();
+}
+
 int ca_select_scores(const ca_dims* dims, const void* scores, int32_t dtype, int64_t stride_b,
                      int64_t stride_h, int64_t stride_q, const ca_select_rule* rule,
                      const int32_t* past_blocks_host, uint32_t* rowmask, void* stream) {

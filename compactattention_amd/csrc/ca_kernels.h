@@ -67,6 +67,13 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
                                uint32_t* rowmask, float* scores_out, hipStream_t stream);
 
 size_t union_lds_bytes(const Shape& s);
+
+// FlashPrefill per-token block scores (the reference's compute_block_score_chunked +
+// normalize_scores) in block_size (64 or 128) token blocks; s.cap = key blocks per row of the
+// scores, khat rows hold khat_stride block means.
+size_t token_mass_lds_bytes(const Shape& s);
+hipError_t launch_token_mass(const Shape& s, const SeqAddr& q, const float* khat, int64_t khat_stride, int bs,
+                             float scale, const PastBlocks& pb, float* scores, hipStream_t stream);
 constexpr int kCsrRowsMax = 8192;
 hipError_t launch_table_csr(const int32_t* table, int64_t table_stride, const int32_t* counts, int rows, int cap,
                             int32_t* indptr, int32_t* indices, int32_t* last_page_len, hipStream_t stream);

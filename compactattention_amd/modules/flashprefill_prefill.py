@@ -19,7 +19,10 @@ min_budget and last_n_block count 128-token blocks, as in the reference) and nam
 of 128 tokens.
 
 Scores are the pooled softmax of flash_prefill_score_chunked_from_mean_k (see
-compactattention_amd.flashprefill_vendor).  A first chunk (kv_len == q_len) runs dense causal
+compactattention_amd.flashprefill_vendor) by default; score_mode="token" (a keyword of this
+build) scores the chunk's query tokens against the key means as the reference's
+compute_block_score_chunked + normalize_scores do (flashprefill_native_forward.py:98-207,
+365-374), on bf16 MFMAs.  A first chunk (kv_len == q_len) runs dense causal
 attention on the same HIP kernel (identity tables); q_len <= 1 attends densely through the
 decode kernel, where the reference calls its dense backend (q_len <= 1 or kv_len <= q_len,
 :903-907).  A chunk whose length is not a multiple of the block size selects and attends with
@@ -69,34 +72,64 @@ def expand_pair_tables(table: torch.Tensor, counts: torch.Tensor, key_blocks: in
     return out, cnt.to(torch.int32)
 
 
+SCORE_MODES = ("pooled", "token")
+
+
+def check_score_mode(score_mode: str) -> None:
+    if score_mode not in SCORE_MODES:
+        raise ValueError(f"score_mode={score_mode!r}: expected one of {SCORE_MODES}")
+
+
+def token_mass_rowmask(query_states: torch.Tensor, khat: torch.Tensor, past: Sequence[int], num_kv_heads: int,
+                       cap: int, rule: ops.Rule, block_size: int) -> torch.Tensor:
+    """Row masks from the reference's per-token scores (ca_score_token_mass) in block_size blocks:
+    past and cap count block_size blocks, khat holds block_size-token key means."""
+    scale = 1.0 / math.sqrt(128)
+    scores = ops.score_token_mass(query_states, khat.contiguous(), scale, past, num_kv_heads, cap, block_size)
+    return ops.select_scores(scores, rule, past, num_kv_heads, cap, 64 * scores.shape[2])
+
+
 def flashprefill_tables(qhat: torch.Tensor, khat: torch.Tensor, past_blocks: Sequence[int], q_len: int,
                         num_kv_heads: int, kv_cap: int, rule: ops.Rule, block_size: int,
-                        khat_block_size: int = 64) -> Tuple[torch.Tensor, torch.Tensor]:
+                        khat_block_size: int = 64, score_mode: str = "pooled",
+                        query_states: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Per-KV-group tables of 64-token page ids for a chunk of q_len tokens at past_blocks
     (64-token blocks, one value for every request).  qhat [B, Hq, ceil(q_len/64), 128] are the
     chunk's 64-token query means; khat [B, Hkv, >= P + Qb, 128] the key means in
-    khat_block_size-token blocks (a 128-token khat goes straight to the 128-token scoring)."""
+    khat_block_size-token blocks (a 128-token khat goes straight to the 128-token scoring).
+    score_mode "pooled" scores the block means (the bit-reproducible form); "token" scores the
+    chunk's query tokens against the key means as the reference does (query_states
+    [B, q_len, Hq, 128] required, qhat unused)."""
     check_score_block_size(block_size)
+    check_score_mode(score_mode)
+    if score_mode == "token" and query_states is None:
+        raise ValueError("score_mode='token' needs query_states")
     scale = 1.0 / math.sqrt(128)
     P = [int(p) for p in past_blocks]
     if block_size == 64:
-        rowmask, _ = ops.score_select(qhat, khat, scale, rule, P, num_kv_heads, kv_cap)
+        if score_mode == "token":
+            rowmask = token_mass_rowmask(query_states, khat[..., :kv_cap, :], P, num_kv_heads, kv_cap, rule, 64)
+        else:
+            rowmask, _ = ops.score_select(qhat, khat, scale, rule, P, num_kv_heads, kv_cap)
         table, counts, _, _ = ops.union_compact(rowmask, P, num_kv_heads, kv_cap, last_n_block=rule.last_n_block)
         return table, counts
     if len(set(P)) != 1 or P[0] % 2:
         raise ValueError(f"128-token FlashPrefill blocks need a chunk that starts at a multiple of 128 tokens "
                          f"(past {64 * P[0]} tokens)")
-    qb64 = qhat.shape[2]
+    qb64 = -(-q_len // 64)
     last = q_len - 64 * (qb64 - 1)  # tokens of the chunk's last 64-token block
     kb64 = P[0] + qb64
-    q128 = ops.pair_block_summaries(qhat, qb64, last)
+    q128 = ops.pair_block_summaries(qhat, qb64, last) if score_mode == "pooled" else None
     P128 = [P[0] // 2] * len(P)
     cap128 = -(-kb64 // 2)
     if khat_block_size == 128:  # rows of exactly cap128 summaries (the kernels' row stride)
         k128 = khat[..., :cap128, :].contiguous()
     else:
         k128 = ops.pair_block_summaries(khat, kb64, last)
-    rowmask, _ = ops.score_select(q128, k128, scale, rule, P128, num_kv_heads, cap128)
+    if score_mode == "token":
+        rowmask = token_mass_rowmask(query_states, k128, P128, num_kv_heads, cap128, rule, 128)
+    else:
+        rowmask, _ = ops.score_select(q128, k128, scale, rule, P128, num_kv_heads, cap128)
     t128, c128, _, _ = ops.union_compact(rowmask, P128, num_kv_heads, cap128, last_n_block=rule.last_n_block)
     return expand_pair_tables(t128, c128, kb64, kv_cap)
 
@@ -123,8 +156,10 @@ def flashprefill_compactattn_prefill_full_kv(
     k_hf: Optional[torch.Tensor] = None,
     v_hf: Optional[torch.Tensor] = None,
     mean_k_cache: Optional[torch.Tensor] = None,
+    score_mode: str = "pooled",
 ) -> Tuple[torch.Tensor, Dict[str, float]]:
     del attn_module
+    check_score_mode(score_mode)
     if indexed_impl not in INDEXED_IMPLS:
         raise ValueError(f"Unsupported indexed_impl: {indexed_impl}")
     if pack_impl not in PACK_IMPLS:
@@ -184,7 +219,7 @@ def flashprefill_compactattn_prefill_full_kv(
         cap = khat.shape[2] if khat_bs == 64 else geo.kv_cap
         qhat = ops.pool_query(query_states, P, cap, num_kv_heads=geo.num_kv_heads)
         return flashprefill_tables(qhat, khat, P, geo.q_len, geo.num_kv_heads, cap, rule, block_size,
-                                   khat_block_size=khat_bs)
+                                   khat_block_size=khat_bs, score_mode=score_mode, query_states=query_states)
 
     table, counts = timer("flashprefill_select_ms", select)
     out = timer("attention_ms", lambda: attend(query_states, K, V, table, counts, geo, softmax_scale))

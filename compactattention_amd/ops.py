@@ -399,6 +399,29 @@ def score_select(qhat: torch.Tensor, khat: torch.Tensor, scale: float, rule: Rul
     return rowmask, (scores if with_scores else None)
 
 
+def score_token_mass(q: torch.Tensor, khat: torch.Tensor, scale: float, past_blocks: Sequence[int], num_kv_heads: int,
+                     kv_cap: int, block_size: int = 64) -> torch.Tensor:
+    """FlashPrefill per-token block scores (ca_score_token_mass): q [B, Lq, Hq, 128] bf16 and key
+    means khat [B*Hkv or B x Hkv, >= kv_cap, 128] fp32 in block_size-token blocks; past_blocks
+    and kv_cap count block_size blocks.  Returns [B, Hq, ceil(Lq/block_size), kv_cap] fp32."""
+    _need_cuda("khat", khat, torch.float32)
+    if khat.shape[-1] != HEAD_DIM or khat.stride(-1) != 1 or khat.stride(-2) != HEAD_DIM:
+        raise ValueError("khat must hold contiguous rows of 128-float block means")
+    B, Lq, Hq, _ = q.shape
+    rows = B * num_kv_heads
+    stride_blocks = khat.stride(-3) // HEAD_DIM if khat.dim() >= 3 else kv_cap
+    if khat.numel() < rows * stride_blocks * HEAD_DIM or not khat.is_contiguous():
+        raise ValueError("khat must be contiguous [B*Hkv, blocks, 128]")
+    d = make_dims(B, Lq, Hq, num_kv_heads, kv_cap)
+    ql = seq_layout(q, "q")
+    qb = -(-Lq // block_size)
+    scores = torch.empty((B, Hq, qb, kv_cap), dtype=torch.float32, device=q.device)
+    check(_hip.lib().ca_score_token_mass(ctypes.byref(d), ctypes.byref(ql), khat.data_ptr(), int(stride_blocks),
+                                         int(block_size), float(scale), past_array(past_blocks, d.batch),
+                                         scores.data_ptr(), _stream()))
+    return scores
+
+
 def select_scores(scores: torch.Tensor, rule: Rule, past_blocks: Sequence[int], num_kv_heads: int, kv_cap: int,
                   q_len: int) -> torch.Tensor:
     """Caller scores [B, Hq, Qb, >= P+Qb] (fp32 or bf16, last dim contiguous) -> rowmask."""

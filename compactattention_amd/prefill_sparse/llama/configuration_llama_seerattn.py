@@ -60,6 +60,9 @@ class SeerAttnLlamaConfig:
     seerattn_flashprefill_alpha: float = 0.06
     seerattn_flashprefill_last_n_block: int = 2
     seerattn_flashprefill_min_budget: int = 0
+    # this build's choice of FlashPrefill score form: "pooled" (block means, bit-reproducible)
+    # or "token" (the reference's per-token exp2 mass, compute_block_score_chunked)
+    seerattn_flashprefill_score_mode: str = "pooled"
 
     @classmethod
     def from_dict(cls, d: Dict[str, Any]) -> "SeerAttnLlamaConfig":
@@ -85,6 +88,8 @@ class SeerAttnLlamaConfig:
             raise ValueError("the compactattn path runs 64-token blocks")
         if self.seerattn_flashprefill_block_size not in (64, 128):
             raise ValueError("FlashPrefill scoring runs 64- or 128-token blocks")
+        if self.seerattn_flashprefill_score_mode not in ("pooled", "token"):
+            raise ValueError("seerattn_flashprefill_score_mode must be 'pooled' or 'token'")
         from ..attn_gate import parse_gate_type
 
         parse_gate_type(self.seerattn_gate_type)

@@ -93,7 +93,9 @@ class LlamaFlashPrefillCompactAttnAttention(nn.Module):
             else:  # score blocks of seerattn_flashprefill_block_size (64 or 128) tokens
                 table, counts = flashprefill_tables(qhat, cache.kmean, P, L, self.num_key_value_heads, cache.cap,
                                                     self._selection_rule(),
-                                                    self.config.seerattn_flashprefill_block_size)
+                                                    self.config.seerattn_flashprefill_block_size,
+                                                    score_mode=self.config.seerattn_flashprefill_score_mode,
+                                                    query_states=query_states)
             K, V = cache.layouts()
             out = ops.attn_fwd(query_states, K, V, table, counts, P, self.scaling, cache.cap,
                                self.num_key_value_heads)

@@ -233,6 +233,30 @@ int ca_score_select(const ca_dims* dims, const float* qhat, const float* khat, f
                     float* scores, void* stream);
 
 /*
+ * FlashPrefill block scores in the reference's per-token form: for every request b, Q head h,
+ * query block qb and key block kb, the exp2 mass over the block's token slots t of
+ *     s = dot(q_t, bf16(khat[b, h/G, kb])) * scale * log2(e)
+ * taken where the whole key block precedes the token (64 P_b + block_size qb + t >=
+ * block_size (kb + 1) - 1), shifted by its maximum over t, then normalised over the row:
+ *     score = mass * exp2(max - rowmax) / (sum_kb of that + 1e-9).
+ * Blocks here are block_size (64 or 128) tokens: past_blocks_host and dims->kv_cap count
+ * block_size blocks (the chunk starts at past_blocks * block_size); the row's key blocks are
+ * nk = P_b + ceil(q_len / block_size) <= kv_cap, and the chunk's last block keeps the slots
+ * past q_len as zero queries, as the reference does.  q has the ca_seq_layout of the chunk's
+ * queries; khat [B*Hkv, khat_stride, 128] fp32 block means (rounded to bf16 for the products,
+ * as the reference stores them); scores [B, Hq, ceil(q_len/block_size), kv_cap] fp32 receives
+ * the scores (0 past nk).  Products on bf16 MFMAs with fp32 accumulation: the scores agree
+ * with an fp64 evaluation of the same formula to a few ulps, not bit for bit.  The pooled
+ * scores of ca_score_select remain the bit-reproducible form; these feed ca_select_scores.
+ * Replaces: compute_block_score_chunked (K_STRIDE = block_size) + normalize_scores
+ * (compact_attn/flashprefill_vendor/flashprefill_native_forward.py:98-207,365-374) as
+ * flash_prefill_score_chunked_from_mean_k runs them (:562-582).
+ */
+int ca_score_token_mass(const ca_dims* dims, const ca_seq_layout* q, const float* khat, int64_t khat_stride,
+                        int32_t block_size, float scale, const int32_t* past_blocks_host, float* scores,
+                        void* stream);
+
+/*
  * Per-row selection from caller-provided scores, element (b, h, qb, kb) at
  * scores + b*stride_b + h*stride_h + qb*stride_q + kb (dtype 0 = fp32, 1 = bf16).  The score
  * columns cover kb in [0, P_b + Qb); causal as above.  Output as ca_score_select.

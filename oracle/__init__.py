@@ -203,6 +203,59 @@ def block_scores(qhat: np.ndarray, khat: np.ndarray, past_blocks, scale: float) 
     return out
 
 
+def token_mass_scores(q_bits: np.ndarray, khat: np.ndarray, past_blocks, scale: float, block_size: int,
+                      kv_cap: int) -> np.ndarray:
+    """FlashPrefill per-token block scores in fp64, restating compute_block_score_chunked with
+    K_STRIDE = BLOCK_SIZE (compact_attn/flashprefill_vendor/flashprefill_native_forward.py:98-207)
+    and normalize_scores (:365-374).
+
+    q_bits [B, Lq, Hq, 128] bf16 bits; khat [B, Hkv, >= nk, 128] fp32 block means, rounded to
+    bf16 as the reference stores mean_k (:436-443); past_blocks in block_size-token blocks.  For
+    query block qb the token slots t < block_size sit at absolute positions
+    start + qb*BS + t (start = P*BS; slots past Lq hold zero queries, :159-163); key block kb is
+    scored for kb < hi = min(ceil((qmax + 1) / BS), nk) (:166) and seen by slot t when
+    start + qb*BS + t >= kb*BS + BS - 1 (:175-177).  Returns [B, Hq, ceil(Lq/BS), kv_cap]
+    float64 (0 past nk)."""
+    q = bf16_bits_to_f32(q_bits).astype(np.float64)
+    kb16 = bf16_bits_to_f32(f32_to_bf16_bits(np.asarray(khat, dtype=np.float32))).astype(np.float64)
+    B, Lq, Hq, _ = q.shape
+    Hkv = kb16.shape[1]
+    G = Hq // Hkv
+    BS = int(block_size)
+    Qb = -(-Lq // BS)
+    sm = float(scale) * 1.4426950408889634
+    out = np.zeros((B, Hq, Qb, kv_cap), dtype=np.float64)
+    for b in range(B):
+        P = int(past_blocks[b])
+        start = P * BS
+        nk = P + Qb
+        for h in range(Hq):
+            kbf = kb16[b, h // G]
+            for qb in range(Qb):
+                qt = np.zeros((BS, D))
+                n_valid = min(BS, Lq - qb * BS)
+                qt[:n_valid] = q[b, qb * BS:qb * BS + n_valid, h]
+                qabs = start + qb * BS + np.arange(BS)
+                qmax = start + qb * BS + BS - 1
+                hi = min(-(-(qmax + 1) // BS), nk)
+                m = np.full(kv_cap, -np.inf)
+                mass = np.zeros(kv_cap)
+                if hi > 0:
+                    s = (qt @ kbf[:hi].T) * sm  # [BS, hi]
+                    causal = qabs[:, None] >= (np.arange(hi) * BS + BS - 1)[None, :]
+                    s = np.where(causal, s, -np.inf)
+                    mk = s.max(axis=0)
+                    with np.errstate(invalid="ignore"):
+                        e = np.where(causal, np.exp2(s - mk[None, :]), 0.0)
+                    m[:hi] = mk
+                    mass[:hi] = e.sum(axis=0)
+                ok = m[:nk] != -np.inf
+                M = m[:nk].max()
+                sc = np.where(ok, mass[:nk] * np.exp2(np.where(ok, m[:nk] - M, 0.0)), 0.0)
+                out[b, h, qb, :nk] = sc / (sc.sum() + 1e-9)
+    return out
+
+
 def select_rows(scores: np.ndarray, past_blocks, rule: Rule) -> np.ndarray:
     s = np.ascontiguousarray(scores, dtype=np.float32)
     B, Hq, Qb, cap = s.shape
