@@ -7,7 +7,9 @@ never imports it.
 
 The numerics live in ``ca_oracle.c`` (fixed fp32 evaluation order, explicit
 fmaf); this module is a numpy front end over ctypes.  bf16 tensors travel as
-``np.uint16`` bit patterns.
+``np.uint16`` bit patterns.  One function is numpy fp64 instead:
+``token_mass_scores`` (the reference's per-token FlashPrefill scores, which the product
+computes on MFMAs and matches to a tolerance, not bit for bit).
 """
 from __future__ import annotations
 
