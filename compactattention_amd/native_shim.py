@@ -93,11 +93,9 @@ def build_keep_curr_fast_cuda(*, attn_gate_score: torch.Tensor, threshold: float
     (a row mask holds no column past its causal edge, so the OR over all query blocks is the
     reference's OR over q >= c)."""
     rowmask = _row_masks(attn_gate_score, threshold, past_k_blocks)
-    any_q = rowmask[:, :, 0].clone()
-    for q in range(1, rowmask.shape[2]):
-        any_q |= rowmask[:, :, q]
     cols = torch.arange(past_k_blocks, past_k_blocks + curr_k_blocks, device=rowmask.device)
-    return ((any_q[:, :, cols // 32] >> (cols % 32)) & 1).bool()
+    bits = (rowmask[:, :, :, cols // 32] >> (cols % 32)) & 1  # [B, H, Qb, C]
+    return bits.any(dim=2)
 
 
 def build_selected_indices_from_kv_keep_block_cuda_out(*, keep_block_kv: torch.Tensor,
