@@ -61,7 +61,50 @@ def parse():
                     help="only the config-3 Seer model prefill (one JSON line; for kernel traces of the model)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three plain 256 MiB device copies (the HBM counter calibration under rocprofv3)")
+    ap.add_argument("--launch-floor", action="store_true",
+                    help="only time three dependent trivial kernels at the selection kernels' grid (one JSON line; "
+                         "for kernel traces of the per-launch floor)")
     return ap.parse_args()
+
+
+# 512 workgroups of 256 threads for torch's vectorised element-wise kernel (4 elements per
+# thread): the grid of block_logits_kernel and row_select_reg_kernel at config 2
+FLOOR_ELEMS = 512 * 256 * 4
+
+
+def launch_floor(torch) -> dict:
+    """Device time of three dependent trivial kernels (an in-place add over FLOOR_ELEMS floats,
+    one 16-byte load and store per thread) from HIP-graph replays: the fixed cost that three
+    dependent launches of the selection stages pay before any work."""
+    x = torch.zeros(FLOOR_ELEMS, dtype=torch.float32, device="cuda:0")
+    reps, replays = 10, 20
+    for _ in range(3):
+        x.add_(1.0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        x.add_(1.0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            x.add_(1.0)
+            x.add_(1.0)
+            x.add_(1.0)
+    g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(replays):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us3 = e0.elapsed_time(e1) / (reps * replays) * 1e3
+    return {"us_per_3_launches": round(us3, 2), "us_per_launch": round(us3 / 3, 2), "elements": FLOOR_ELEMS,
+            "graph_reps": reps, "replays": replays}
 
 
 def main() -> int:
@@ -79,6 +122,9 @@ def main() -> int:
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes": a.numel(), "copies": 3}))
+        return 0
+    if args.launch_floor:
+        print(json.dumps({"launch_floor": launch_floor(torch)}))
         return 0
 
     from compactattention_amd import ops
@@ -228,6 +274,10 @@ def main() -> int:
         "attention": lambda: ops.attn_fwd(q, K, V, table, counts, P, scale, cap, HKV, out=out, num_splits=splits,
                                           workspace=ws),
     }
+    floor_x = torch.zeros(FLOOR_ELEMS, dtype=torch.float32, device=dev)
+    # three dependent trivial launches at the selection kernels' grid: what score + select +
+    # union pay in launches before any work (compare score_select + union_compact)
+    stage_fns["launch_floor_3"] = lambda: (floor_x.add_(1.0), floor_x.add_(1.0), floor_x.add_(1.0))
     # eager per-call times (launch stream events; the small stages are bound by the host's
     # launch rate here) and device times from graph replays
     stage_us_eager = {k: timed(fn) for k, fn in stage_fns.items()}
