@@ -424,7 +424,7 @@ int ca_score_token_mass(const ca_dims* dims, const ca_seq_layout* q, const float
     for (int b = 0; b < s.B; ++b)
         if ((int64_t)past_blocks_host[b] * block_size > ((int64_t)1 << 30))
             return fail(CA_ERR_LIMIT, "past_blocks[%d]=%d: positions beyond 2^30 tokens", b, past_blocks_host[b]);
-    if (ca::token_mass_lds_bytes(s) > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap=%d too large", s.cap);
+    if (ca::token_mass_lds_bytes(s, block_size) > kMaxLds) return fail(CA_ERR_LIMIT, "kv_cap=%d too large", s.cap);
     hipError_t e = ca::launch_token_mass(s, qa, khat, khat_stride, block_size, scale, pb, scores,
                                          static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "score_token_mass launch");

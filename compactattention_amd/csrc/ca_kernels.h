@@ -71,7 +71,7 @@ size_t union_lds_bytes(const Shape& s);
 // FlashPrefill per-token block scores (the reference's compute_block_score_chunked +
 // normalize_scores) in block_size (64 or 128) token blocks; s.cap = key blocks per row of the
 // scores, khat rows hold khat_stride block means.
-size_t token_mass_lds_bytes(const Shape& s);
+size_t token_mass_lds_bytes(const Shape& s, int bs);
 hipError_t launch_token_mass(const Shape& s, const SeqAddr& q, const float* khat, int64_t khat_stride, int bs,
                              float scale, const PastBlocks& pb, float* scores, hipStream_t stream);
 constexpr int kCsrRowsMax = 8192;
