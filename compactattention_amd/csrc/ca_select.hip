@@ -294,19 +294,19 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
         constexpr int kQIters = 64 * (kD / 4) / 256;
         constexpr int kKIters = KT * (kD / 4) / 256;
         float4 qv[kQIters], kv[kKIters];
+        // unconditional loads (rows past the tile's last valid row re-read that row; their
+        // logits are computed and never stored), so all of them are in flight at once
 #pragma unroll
         for (int i = 0; i < kQIters; ++i) {
             const int f = t + 256 * i;
             const int r = f >> 5, c4 = f & 31;
-            qv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < mrows) qv[i] = *reinterpret_cast<const float4*>(qbase + (int64_t)r * kD + c4 * 4);
+            qv[i] = *reinterpret_cast<const float4*>(qbase + (int64_t)min(r, mrows - 1) * kD + c4 * 4);
         }
 #pragma unroll
         for (int i = 0; i < kKIters; ++i) {
             const int f = t + 256 * i;
             const int r = f >> 5, c4 = f & 31;
-            kv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < krows) kv[i] = *reinterpret_cast<const float4*>(kbase + (int64_t)r * kD + c4 * 4);
+            kv[i] = *reinterpret_cast<const float4*>(kbase + (int64_t)min(r, krows - 1) * kD + c4 * 4);
         }
 #pragma unroll
         for (int i = 0; i < kQIters; ++i) {
@@ -774,11 +774,12 @@ __global__ __launch_bounds__(kSelThreads) void row_select_reg_kernel(SelectParam
     float v[NR];  // logits, then probabilities (compute mode); caller scores (select mode)
     if (kCompute) {
         float* srow = p.scores + (int64_t)rid * cap;
+        // unconditional loads of a clamped column (n >= 1), all in flight at once
 #pragma unroll
-        for (int i = 0; i < NR; ++i) {
-            const int kb = t + kSelThreads * i;
-            v[i] = kb < n ? srow[kb] : kNegInf;
-        }
+        for (int i = 0; i < NR; ++i) v[i] = srow[min(t + kSelThreads * i, n - 1)];
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+            if (t + kSelThreads * i >= n) v[i] = kNegInf;
         float m = kNegInf;
 #pragma unroll
         for (int i = 0; i < NR; ++i) m = fmaxf(m, v[i]);
@@ -828,17 +829,19 @@ __global__ __launch_bounds__(kSelThreads) void row_select_reg_kernel(SelectParam
         }
     } else {
         const int64_t off = b * p.ssb + h * p.ssh + qb * p.ssq;
+        // unconditional loads of a clamped column (n >= 1), all in flight at once
+        if (p.dtype == 0) {
+            const float* in = static_cast<const float*>(p.scores_in) + off;
 #pragma unroll
-        for (int i = 0; i < NR; ++i) {
-            const int kb = t + kSelThreads * i;
-            v[i] = 0.0f;
-            if (kb < n) {
-                if (p.dtype == 0)
-                    v[i] = static_cast<const float*>(p.scores_in)[off + kb];
-                else
-                    v[i] = bf16_to_f32(static_cast<const uint16_t*>(p.scores_in)[off + kb]);
-            }
+            for (int i = 0; i < NR; ++i) v[i] = in[min(t + kSelThreads * i, n - 1)];
+        } else {
+            const uint16_t* in = static_cast<const uint16_t*>(p.scores_in) + off;
+#pragma unroll
+            for (int i = 0; i < NR; ++i) v[i] = bf16_to_f32(in[min(t + kSelThreads * i, n - 1)]);
         }
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+            if (t + kSelThreads * i >= n) v[i] = 0.0f;
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
             const int kb = t + kSelThreads * i;
