@@ -377,12 +377,13 @@ def main() -> int:
         },
     }
 
-    if not args.no_cpu_baseline:
-        progress("cpu baseline")
-        result["cpu_baseline"] = cpu_baseline(ch, topk, args.cpu_reps)
     if not args.no_ragged:
         progress("ragged batch")
         result["ragged_batch"] = ragged_batch(dev)
+    if not args.no_cpu_baseline:
+        progress("cpu baseline")
+        ragged_topk = result["ragged_batch"]["topk_per_row"] if "ragged_batch" in result else 3
+        result["cpu_baseline"] = cpu_baseline(ch, topk, args.cpu_reps, ragged_topk)
     if not args.no_decode:
         progress("decode")
         result["decode"] = decode_lines(dev)
@@ -1002,11 +1003,13 @@ def _time_cpu(fn, reps: int):
     return statistics.median(runs), statistics.mean(runs), runs
 
 
-def cpu_baseline(ch, topk, reps: int = 3):
+def cpu_baseline(ch, topk, reps: int = 3, ragged_topk: int = 3):
     """The fp32 PyTorch restatement of the chunk step (oracle/torch_ref.py: cache update, mean-K,
     pooled scores, top-k + sink + local selection, unions, attention over the selected blocks;
     BLAS-backed GEMMs) on the host cores, timed on config 2's whole layer-chunk (the bench's
-    own inputs and top-k) and on BASELINE config 0 in full.  Reported only."""
+    own inputs and top-k), on BASELINE config 0 in full, on config 4's four requests (one chunk
+    step each, at the GPU line's top-k) and, for config 3, on one decoder layer-chunk at the
+    prompt's mean past, extrapolated to the whole prefill.  Reported only."""
     import os
 
     import torch
@@ -1048,6 +1051,9 @@ def cpu_baseline(ch, topk, reps: int = 3):
             best = (k, r)
     topk0, keep0 = best
     med0, mean0, runs0 = _time_cpu(lambda: torch_ref.chunk_step(*args0, topk=topk0), reps)
+    del args0
+    cfg4 = _cpu_config4(ragged_topk, reps)
+    cfg3 = _cpu_config3(reps)
     return {
         "value": round(med2, 1),
         "unit": "us per chunk",
@@ -1063,7 +1069,93 @@ def cpu_baseline(ch, topk, reps: int = 3):
                     "topk": topk0, "keep_ratio": round(keep0, 4),
                     "workload": "config 0 in full: 256 queries over 8192 keys, 32 / 8 heads, fp32, planted inputs "
                                 "(seed 1234), pooled top-k + sink + 2 local blocks at about 25 % keep"},
+        "config4": cfg4,
+        "config3_extrapolated": cfg3,
     }
+
+
+def _cpu_config4(topk: int, reps: int) -> dict:
+    """Config 4 on the host: the four requests' chunk steps (28 / 4 heads, 512-token chunks over
+    16K / 48K / 96K / 128K cached tokens) one after another, each on all cores, at the GPU
+    line's per-row top-k; the batch time is their sum."""
+    import torch
+
+    from compactattention_amd.synthetic import make_chunk
+    from oracle import torch_ref
+
+    pasts, lq, hq, hkv = (16384, 49152, 98304, 131072), 512, 28, 4
+    per_req, keeps = [], []
+    for i, past in enumerate(pasts):
+        c = make_chunk([past], lq, hq, hkv, seed=1234 + i)
+        P = c.past_blocks[0]
+        q = c.q.float()
+        k = c.k[:, :, :past + lq].float()
+        v = c.v[:, :, :past + lq].float()
+        del c
+        k_new = k[:, :, past:].transpose(1, 2).contiguous()
+        v_new = v[:, :, past:].transpose(1, 2).contiguous()
+        k_past, v_past = k[:, :, :past].contiguous(), v[:, :, :past].contiguous()
+        del k, v
+        kmean = torch_ref.block_means(k_past.transpose(1, 2))
+        med, _, _ = _time_cpu(lambda: torch_ref.chunk_step(q, k_past, v_past, k_new, v_new, kmean, topk=topk), reps)
+        tabs = torch_ref.chunk_step(q, k_past, v_past, k_new, v_new, kmean, topk=topk)[4]
+        keeps.append(sum(len(t) - lq // 64 for t in tabs) / (len(tabs) * P))
+        per_req.append(round(med, 1))
+        del q, k_past, v_past, k_new, v_new, kmean
+    return {"median_us": round(sum(per_req), 1), "per_request_median_us": per_req, "topk": topk,
+            "keep_ratio": round(sum(keeps) / len(keeps), 4),
+            "workload": "config 4: four requests (16K / 48K / 96K / 128K cached tokens, 512-token chunks, 28 / 4 "
+                        "heads), one fp32 chunk step each (1 warm-up + runs, median), summed"}
+
+
+def _cpu_config3(reps: int) -> dict:
+    """Config 3 extrapolated: one Llama-3.1-8B decoder layer-chunk (2048 tokens; RMSNorm, q/k/v,
+    RoPE, pooled top-k selection at about 25 % keep, sparse attention, o_proj, SwiGLU MLP) over
+    the prompt's mean past (64K tokens) on the host, times 32 layers x 64 chunks.  The linear
+    layers' cost is the same at every chunk and the selected attention grows linearly with the
+    past, so the mean past gives the mean layer-chunk.  Labelled an extrapolation: the whole
+    prefill (about 3 PFLOP) is not run on the CPU."""
+    import math
+
+    import torch
+
+    from oracle import torch_ref
+
+    hid, hq, hkv, inter, lq, past, layers, chunks = 4096, 32, 8, 14336, 2048, 65536, 32, 64
+    g = torch.Generator().manual_seed(1234)
+
+    def W(o, i):
+        return torch.randn((o, i), generator=g) * 0.02
+
+    w = {"ln1": torch.ones(hid), "wq": W(hq * 128, hid), "wk": W(hkv * 128, hid), "wv": W(hkv * 128, hid),
+         "wo": W(hid, hq * 128), "ln2": torch.ones(hid), "wg": W(inter, hid), "wu": W(inter, hid), "wd": W(hid, inter)}
+    h = torch.randn((1, lq, hid), generator=g)
+    k_past = torch.randn((1, hkv, past, 128), generator=g)
+    v_past = torch.randn((1, hkv, past, 128), generator=g)
+    kmean = torch_ref.block_means(k_past.transpose(1, 2))
+    # top-k per row for about 25 % of the past after the unions (the GPU line's operating
+    # point), calibrated on the layer's own queries and keys
+    P, qb = past // 64, lq // 64
+    pos = past + torch.arange(lq)
+    x = torch_ref.rms_norm(h, w["ln1"])
+    qhat = torch_ref.block_means(torch_ref.rope((x @ w["wq"].T).view(1, lq, hq, 128), pos))
+    khat = torch.cat([kmean, torch_ref.block_means(torch_ref.rope((x @ w["wk"].T).view(1, lq, hkv, 128), pos))], dim=2)
+    del x
+    best = None
+    for k in (1, 2, 3, 4, 6, 8, 12, 16, 24, 32):
+        tabs = torch_ref.select_tables(qhat, khat, P, k, 1, 2, 1 / math.sqrt(128))
+        r = sum(len(t) - qb for t in tabs) / (len(tabs) * P)
+        if best is None or abs(r - 0.25) < abs(best[1] - 0.25):
+            best = (k, r)
+    topk, keep = best
+    med, mean, runs = _time_cpu(lambda: torch_ref.decoder_layer_step(h, w, k_past, v_past, kmean, hq, hkv, topk), reps)
+    total_s = med * 1e-6 * layers * chunks
+    return {"layer_chunk_median_us": round(med, 1), "layer_chunk_mean_us": round(mean, 1),
+            "runs": [round(x, 1) for x in runs], "topk": topk, "keep_ratio_calibration": round(keep, 4),
+            "extrapolated_seconds": round(total_s, 1), "extrapolated_tok_per_s": round(chunks * lq / total_s, 1),
+            "workload": "config 3 extrapolated (not run whole): one decoder layer-chunk of the Llama-3.1-8B shape "
+                        "(2048 tokens over 65536 cached, random N(0,0.02) fp32 weights, pooled top-k at ~25 % keep), "
+                        "times 32 layers x 64 chunks"}
 
 
 if __name__ == "__main__":

@@ -20,6 +20,11 @@ reference's own path cannot run on a CPU: it needs flash_attn, CUDA and Triton):
   5. attention of every query over its KV row's selected blocks with bottom-right causal
      masking (indexed_dense_prefill_direct_triton.py:91-241 semantics): gather, q k^T,
      softmax, PV.
+
+decoder_layer_step wraps chunk_step in one Llama decoder layer (RMSNorm, q/k/v projections,
+rotate_half RoPE, o_proj and the residual, RMSNorm, SwiGLU MLP), the layer the reference's
+compactattn models run per chunk (modeling_llama_seerattn_chunked_dense.py:547-938 around the
+attention call); bench.py times it for the whole-model (config 3) CPU extrapolation.
 """
 from __future__ import annotations
 
@@ -93,3 +98,39 @@ def chunk_step(q: torch.Tensor, k_past: torch.Tensor, v_past: torch.Tensor, k_ne
     tables = select_tables(block_means(q), kmean_all, past, topk, sink, local, scale)
     out = attention(q, k_all, v_all, tables, past, scale)
     return out, k_all, v_all, kmean_all, tables
+
+
+def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """Llama RMSNorm in fp32: x / sqrt(mean(x^2) + eps) * w."""
+    return x * torch.rsqrt(x.pow(2).mean(dim=-1, keepdim=True) + eps) * w
+
+
+def rope(x: torch.Tensor, pos: torch.Tensor, theta: float = 500000.0) -> torch.Tensor:
+    """rotate_half RoPE (compact_attn/modules/common.py:29-81 convention): x [B, L, H, D] at
+    positions pos [L]."""
+    D = x.shape[-1]
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float64) / D))
+    ang = pos.double()[:, None] * inv[None, :]
+    cos = torch.cat([ang.cos(), ang.cos()], dim=-1).float()[None, :, None, :]
+    sin = torch.cat([ang.sin(), ang.sin()], dim=-1).float()[None, :, None, :]
+    x1, x2 = x[..., :D // 2], x[..., D // 2:]
+    return x * cos + torch.cat([-x2, x1], dim=-1) * sin
+
+
+def decoder_layer_step(h: torch.Tensor, w: dict, k_past: torch.Tensor, v_past: torch.Tensor,
+                       kmean_past: torch.Tensor, num_q_heads: int, num_kv_heads: int, topk: int
+                       ) -> torch.Tensor:
+    """One Llama decoder layer over a chunk h [B, L, hidden] fp32 whose past K/V (heads-first,
+    [B, Hkv, P*64, 128]) and mean-K are cached: the attention is chunk_step's selection and
+    sparse attention.  w holds ln1, wq, wk, wv, wo, ln2, wg, wu, wd ([out, in] like nn.Linear)."""
+    B, L, _ = h.shape
+    D = 128
+    pos = k_past.shape[2] + torch.arange(L)
+    x = rms_norm(h, w["ln1"])
+    q = rope((x @ w["wq"].T).view(B, L, num_q_heads, D), pos)
+    k = rope((x @ w["wk"].T).view(B, L, num_kv_heads, D), pos)
+    v = (x @ w["wv"].T).view(B, L, num_kv_heads, D)
+    out = chunk_step(q, k_past, v_past, k, v, kmean_past, topk)[0]
+    h = h + out.reshape(B, L, num_q_heads * D) @ w["wo"].T
+    x = rms_norm(h, w["ln2"])
+    return h + (torch.nn.functional.silu(x @ w["wg"].T) * (x @ w["wu"].T)) @ w["wd"].T

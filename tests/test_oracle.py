@@ -576,3 +576,56 @@ def test_torch_restatement_matches_oracle():
         assert tables[r].tolist() == tab[r, :cnt[r]].tolist()
     ref = oracle.attention(qb, kb, vb, [P], tab, cnt, 1 / math.sqrt(128))
     assert np.abs(out.numpy() - ref).max() <= 1e-4
+
+
+def test_torch_restatement_rope_and_layer():
+    """The CPU decoder layer timed for the config-3 extrapolation (oracle/torch_ref.py):
+    - rope rotates each (x_i, x_{i+64}) pair by pos * theta^(-2i/128), checked element by
+      element in fp64;
+    - decoder_layer_step with every past block kept equals a dense layer written here with
+      torch SDPA (pre-norm residual blocks, SwiGLU), so norm placement, residuals and the
+      projection layout are pinned; a planted mistake (the MLP without its RMSNorm) fails."""
+    from oracle import torch_ref
+
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn((1, 6, 2, 128), generator=g)
+    pos = torch.arange(6) + 1000
+    y = torch_ref.rope(x, pos).double()
+    inv = 1.0 / (500000.0 ** (torch.arange(0, 128, 2, dtype=torch.float64) / 128))
+    ang = pos.double()[:, None] * inv[None, :]  # [L, 64]
+    c, s = ang.cos()[None, :, None, :], ang.sin()[None, :, None, :]
+    xd = x.double()
+    ref = torch.cat([xd[..., :64] * c - xd[..., 64:] * s, xd[..., 64:] * c + xd[..., :64] * s], dim=-1)
+    assert torch.allclose(y, ref, atol=1e-5)
+
+    hid, hq, hkv, inter, L, past = 256, 4, 2, 384, 64, 128
+    D = 128
+
+    def W(o, i):
+        return torch.randn((o, i), generator=g) * 0.05
+
+    w = {"ln1": 1 + 0.1 * torch.randn(hid, generator=g), "wq": W(hq * D, hid), "wk": W(hkv * D, hid),
+         "wv": W(hkv * D, hid), "wo": W(hid, hq * D), "ln2": 1 + 0.1 * torch.randn(hid, generator=g),
+         "wg": W(inter, hid), "wu": W(inter, hid), "wd": W(hid, inter)}
+    h = torch.randn((1, L, hid), generator=g)
+    k_past = torch.randn((1, hkv, past, D), generator=g)
+    v_past = torch.randn((1, hkv, past, D), generator=g)
+    kmean_past = torch_ref.block_means(k_past.transpose(1, 2))
+    got = torch_ref.decoder_layer_step(h, w, k_past, v_past, kmean_past, hq, hkv, topk=past // 64)
+
+    def dense_layer(mlp_norm=True):
+        p = torch.arange(L) + past
+        x = torch_ref.rms_norm(h, w["ln1"])
+        q = torch_ref.rope((x @ w["wq"].T).view(1, L, hq, D), p).transpose(1, 2)
+        k = torch_ref.rope((x @ w["wk"].T).view(1, L, hkv, D), p).transpose(1, 2)
+        v = (x @ w["wv"].T).view(1, L, hkv, D).transpose(1, 2)
+        k = torch.cat([k_past, k], dim=2).repeat_interleave(hq // hkv, dim=1)
+        v = torch.cat([v_past, v], dim=2).repeat_interleave(hq // hkv, dim=1)
+        mask = torch.arange(past + L)[None, :] <= (past + torch.arange(L))[:, None]
+        a = torch.nn.functional.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+        hh = h + a.transpose(1, 2).reshape(1, L, hq * D) @ w["wo"].T
+        x = torch_ref.rms_norm(hh, w["ln2"]) if mlp_norm else hh
+        return hh + (torch.nn.functional.silu(x @ w["wg"].T) * (x @ w["wu"].T)) @ w["wd"].T
+
+    assert torch.allclose(got, dense_layer(), atol=1e-4, rtol=1e-4)
+    assert not torch.allclose(got, dense_layer(mlp_norm=False), atol=1e-3, rtol=1e-3)
