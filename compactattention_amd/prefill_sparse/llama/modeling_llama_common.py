@@ -278,7 +278,7 @@ class CompactAttnLlamaModel(nn.Module):
 class CompactAttnLlamaForCausalLM(nn.Module):
     """Decoder + LM head; forward(input_ids, past_key_values, logits_to_keep) runs one
     prefill chunk (the reference runtime's call, chunked_prefill_runtime.py:1168-1203) or,
-    with fewer than 64 tokens or after an unaligned step, one dense decode step."""
+    for a single token or once the cache length is inside a block, one dense decode step."""
 
     attn_cls: Type[nn.Module] = nn.Module
     cache_with_kmean = False
