@@ -68,7 +68,8 @@ __device__ __forceinline__ float tm_xor32_add(float x) {
 
 // MT = 32-token tiles per query block (2 for 64-token blocks, 4 for 128).  LDS: the block's
 // query tile (MT * 32 rows of 256 B, 16-byte chunk c of row r at chunk c ^ (r & 15)), then
-// m[cap], pmass[cap], 16 floats of reductions and 8 KB of key tile per wave.
+// m[cap], pmass[cap] (each padded to a multiple of 4 floats), 16 floats of reductions and
+// 8 KB of key tile per wave.
 template <int MT>
 __global__ __launch_bounds__(kTmWaves * 64) __attribute__((amdgpu_waves_per_eu(2))) void token_mass_kernel(TokenMassParams p) {
     extern __shared__ __attribute__((aligned(16))) float tm_lds[];
@@ -95,9 +96,10 @@ __global__ __launch_bounds__(kTmWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     const int64_t qmax = start + (int64_t)qb * BS + BS - 1;
     const int hi = (int)min((int64_t)nk, (qmax + 1 + BS - 1) / BS);
     uint8_t* qs = reinterpret_cast<uint8_t*>(tm_lds);
+    const int cap4 = (cap + 3) & ~3;  // keeps the arrays after m and p 16-byte aligned
     float* mrow = tm_lds + BS * 64;
-    float* prow = mrow + cap;
-    float* red = prow + cap;
+    float* prow = mrow + cap4;
+    float* red = prow + cap4;
 
     // ---- the query tile into LDS (tokens past q_len are zero slots) ----
     for (int f = tid; f < BS * 16; f += kTmWaves * 64) {
@@ -258,7 +260,8 @@ __global__ __launch_bounds__(kTmWaves * 64) __attribute__((amdgpu_waves_per_eu(2
 }  // namespace
 
 size_t token_mass_lds_bytes(const Shape& s, int bs) {
-    return (size_t)bs * 256 + sizeof(float) * (2 * (size_t)s.cap + 2 * kTmWaves) + 8192 * kTmWaves;
+    const size_t cap4 = ((size_t)s.cap + 3) & ~(size_t)3;
+    return (size_t)bs * 256 + sizeof(float) * (2 * cap4 + 2 * kTmWaves) + 8192 * kTmWaves;
 }
 
 hipError_t launch_token_mass(const Shape& s, const SeqAddr& q, const float* khat, int64_t khat_stride, int bs,
