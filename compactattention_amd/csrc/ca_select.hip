@@ -265,17 +265,24 @@ __global__ __launch_bounds__(256) void chunk_summaries_kernel(Shape s, SeqAddr k
 // each thread owns a 4 x KT/16 register tile and every dot product is one sequential fma
 // chain over d = 0..127.
 constexpr int kPadRow = kD + 4;  // LDS row pitch (floats) for summary tiles
+constexpr int kLogitsGridSlots = 512;  // block-logits workgroups resident at once (2 per CU)
 
 // One workgroup computes a 64-row x KT-key tile of logits (KT = 32: twice the workgroups of
-// 64-key tiles, so the last round of the grid carries half as much work per CU).
+// 64-key tiles, so the last round of the grid carries half as much work per CU).  The first
+// `extra` tiles of a row hold one key more (tile x starts at KT x + min(x, extra)): a row
+// whose keys need just over a multiple of two workgroups per CU stays in one round of the
+// grid instead of spilling a few tiles into a second (config 2: 2064 keys per row as 64
+// tiles, 16 of them of 33 keys).  Wave 0 computes the extra key's 64 logits, one fma chain
+// per row in the same order.
 template <int KT>
 __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float* qhat, const float* khat,
-                                                           float scale, PastBlocks pb, float* logits) {
+                                                           float scale, PastBlocks pb, float* logits, int extra) {
     static_assert(KT == 32 || KT == 64, "16 key groups of KT/16 keys");
     constexpr int KJ = KT / 16;  // keys per thread
     __shared__ __attribute__((aligned(16))) float qt[64 * kPadRow];
-    __shared__ __attribute__((aligned(16))) float kt[KT * kPadRow];
-    const int kb0 = blockIdx.x * KT;
+    __shared__ __attribute__((aligned(16))) float kt[(KT + 1) * kPadRow];
+    const int kb0 = blockIdx.x * KT + min((int)blockIdx.x, extra);
+    const bool has_extra = (int)blockIdx.x < extra;
     const int row = blockIdx.y;
     const int m0 = blockIdx.z * 64;
     const int b = row / s.Hkv;
@@ -288,7 +295,7 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
     const float* qbase = qhat + ((int64_t)(b * s.Hq + hk * s.G) * s.Qb + m0) * kD;
     const float* kbase = khat + ((int64_t)row * s.cap + kb0) * kD;
     const int mrows = min(64, M - m0);
-    const int krows = min(KT, nkb - kb0);
+    const int krows = min(KT + (has_extra ? 1 : 0), nkb - kb0);
     {
         // all loads of a thread in flight before the LDS stores
         constexpr int kQIters = 64 * (kD / 4) / 256;
@@ -320,6 +327,9 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
             const int r = f >> 5, c4 = f & 31;
             *reinterpret_cast<float4*>(kt + r * kPadRow + c4 * 4) = kv[i];
         }
+        if (has_extra && t < 32)  // key KT of the tile (re-read of the last valid row past nkb)
+            *reinterpret_cast<float4*>(kt + KT * kPadRow + t * 4) =
+                *reinterpret_cast<const float4*>(kbase + (int64_t)min(KT, krows - 1) * kD + t * 4);
     }
     __syncthreads();
     const int lane = t & 63;
@@ -359,6 +369,23 @@ __global__ __launch_bounds__(256) void block_logits_kernel(Shape s, const float*
             const int kb = kb0 + KJ * tn + j;
             if (kb <= P + qb) out[kb] = acc[i][j] * scale;
         }
+    }
+    if (has_extra && t < 64) {
+        // key KT of the tile for query row t: the same sequential fma chain over d = 0..127
+        // (after the tile: beside the tile's chains, in every wave, it measured slower)
+        const int m = m0 + t;
+        float v = 0.0f;
+        for (int d = 0; d < kD; d += 4) {
+            const float4 a = *reinterpret_cast<const float4*>(qt + t * kPadRow + d);
+            const float4 c = *reinterpret_cast<const float4*>(kt + KT * kPadRow + d);
+            v = __builtin_fmaf(a.x, c.x, v);
+            v = __builtin_fmaf(a.y, c.y, v);
+            v = __builtin_fmaf(a.z, c.z, v);
+            v = __builtin_fmaf(a.w, c.w, v);
+        }
+        const int kb = kb0 + KT;
+        if (m < M && kb <= P + m % s.Qb)
+            logits[((int64_t)(b * s.Hq + hk * s.G) * s.Qb + m) * s.cap + kb] = v * scale;
     }
 }
 
@@ -1280,8 +1307,20 @@ hipError_t launch_score_select(const Shape& s, const float* qhat, const float* k
         int max_nkb = 0;
         for (int b = 0; b < s.B; ++b) max_nkb = max(max_nkb, pb.p[b] + s.Qb);
         constexpr int kKT = 32;
-        dim3 grid((max_nkb + kKT - 1) / kKT, s.B * s.Hkv, (s.G * s.Qb + 63) / 64);
-        hipLaunchKernelGGL(block_logits_kernel<kKT>, grid, dim3(256), 0, stream, s, qhat, khat, scale, pb, scores);
+        const int rows_z = s.B * s.Hkv * ((s.G * s.Qb + 63) / 64);
+        int tiles = (max_nkb + kKT - 1) / kKT;
+        int extra = 0;
+        // two workgroups on each of the 256 CUs: when the 32-key tiles overflow that by a few
+        // tiles per row, fit the row into kLogitsGridSlots / rows tiles, the first of them
+        // holding 33 keys (at most one more key per tile)
+        const int fit = kLogitsGridSlots / rows_z;
+        if (tiles * rows_z > kLogitsGridSlots && fit >= 1 && fit < tiles && max_nkb <= fit * (kKT + 1)) {
+            tiles = fit;
+            extra = max_nkb - fit * kKT;
+        }
+        dim3 grid(tiles, s.B * s.Hkv, (s.G * s.Qb + 63) / 64);
+        hipLaunchKernelGGL(block_logits_kernel<kKT>, grid, dim3(256), 0, stream, s, qhat, khat, scale, pb, scores,
+                           extra);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

@@ -383,6 +383,30 @@ def test_score_select_row_lengths(gpu, past):
         assert np.array_equal(unpack_rowmask(rowmask, cap), oracle.select_rows(ref_scores, [past], rule))
 
 
+@pytest.mark.parametrize("past,Hkv,G,Lq", [
+    ([2048, 900], 4, 2, 1024),   # 8 rows x 2064 keys: 64 tiles per row, 16 of them of 33 keys
+    ([4100, 3000], 2, 4, 256),   # 4 rows x 4104 keys: 128 tiles per row, 8 of 33 keys
+])
+def test_score_select_tiles_of_33_keys(gpu, past, Hkv, G, Lq):
+    """Block logits whose 32-key tiles would overflow two workgroups per CU fit each row into
+    fewer tiles, the first ones holding 33 keys; a shorter request's tiles end early.  Scores
+    and masks bit for bit against the oracle."""
+    _print_case(test="score_select_33", past=past, Hkv=Hkv, G=G)
+    B = len(past)
+    Hq = Hkv * G
+    cap = max(past) + Lq // 64
+    g = torch.Generator().manual_seed(sum(past))
+    qhat = torch.randn((B, Hq, Lq // 64, 128), generator=g) * 0.3
+    khat = torch.randn((B * Hkv, cap, 128), generator=g) * 0.3
+    scale = 1.0 / math.sqrt(128)
+    rule = oracle.Rule(topk=10, sink_blocks=1, local_blocks=2)
+    rowmask, scores = ops.score_select(qhat.to(gpu), khat.to(gpu), scale, _ops_rule(rule), past, Hkv, cap,
+                                       with_scores=True)
+    ref_scores = oracle.block_scores(qhat.numpy(), khat.numpy().reshape(B, Hkv, cap, 128), past, scale)
+    assert float_bits_equal(f32(scores), ref_scores)
+    assert np.array_equal(unpack_rowmask(rowmask, cap), oracle.select_rows(ref_scores, past, rule))
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_select_scores_ties_and_nonfinite(gpu, dtype):
     _print_case(test="select_scores", dtype=dtype)
