@@ -119,18 +119,25 @@ __global__ __launch_bounds__(kTmWaves * 64) __attribute__((amdgpu_waves_per_eu(2
     // instruction, and the MFMA operands come back with one ds_read_b128 each
     uint8_t* kt = reinterpret_cast<uint8_t*>(red + 2 * kTmWaves) + w * 8192;
     // tile j's key means: 16 float4 per lane, whole rows per instruction (lane l takes float4
-    // l & 31 of keys (l >> 5) + 2 i), all 16 loads issued back to back.  In the last, partial
-    // tile, keys past hi read the last valid key's row (inside the tensor): their columns of
-    // the scores are computed and then dropped (the kvalid test below), so they need no zeroing.
+    // l & 31 of keys (l >> 5) + 2 i), all 16 loads issued back to back through a buffer
+    // resource whose range ends at key hi: keys past it read as zeros (their columns of the
+    // scores are dropped by the kvalid test below), and four 4 KB steps of the vector offset
+    // with the 0 / 1 / 2 / 3 KB instruction offsets address the 16 loads.
     float4 kv[16];
     const int kh = l >> 5, c4 = l & 31;
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(krow), 0, hi * kD * 4, 0x00020000);
+    const int lane_off = kh * (kD * 4) + c4 * 16;
     auto issue_tile = [&](int j) {
         if (j >= ntiles) return;
-        const int nvalid = min(32, hi - 32 * j);
-        const float* tp = krow + (int64_t)(32 * j) * kD + 4 * c4;
+        const int tb = 32 * j * (kD * 4);
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            kv[i] = *reinterpret_cast<const float4*>(tp + min(kh + 2 * i, nvalid - 1) * kD);
+        for (int q = 0; q < 4; ++q) {
+            const int vo = lane_off + tb + q * 4096;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                kv[4 * q + r] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(krs, vo + r * 1024, 0, 0));
+        }
     };
     // LDS byte offsets of key kh + 2 i's float4 c4 (i < 8; key + 16 adds 4096 and keeps the swizzle)
     int soff[8];
