@@ -318,7 +318,7 @@ def main() -> int:
                                   "speedup_vs_dense": round(dense_us / a_us, 3)}
 
     paged = paged_pool_line(dev, q, k_new, v_new, kc, vc, P, cap, HKV, rule, splits, table, counts, flops,
-                            args.steps, timed, graph_timed)
+                            args.steps, args.settle, timed, graph_timed)
 
     # algorithmic HBM bytes of the memory-bound stages
     hbm_bytes = {
@@ -405,12 +405,15 @@ def main() -> int:
     return 0
 
 
-def paged_pool_line(dev, q, k_new, v_new, kc, vc, P, cap, hkv, rule, splits, table, counts, flops, steps, timed,
-                    graph_timed):
+def paged_pool_line(dev, q, k_new, v_new, kc, vc, P, cap, hkv, rule, splits, table, counts, flops, steps, settle,
+                    timed, graph_timed):
     """Config 2 with the cache in a global page pool read through a permuted page table (every
     logical block of every KV row on a random physical page), the same step and inputs as the
     heads-first value: its per-chunk time, graph-replayed path and attention, and whether its
-    output equals the heads-first cache's bit for bit."""
+    output equals the heads-first cache's bit for bit.  Each eager timing follows `settle`
+    seconds of the timed work, as the heads-first value does: the host-side set-up before them
+    leaves the GPU idle long enough for its clock to drop (attention read 621 us against 537 us
+    from a graph right after it, 591 against 592 us once settled)."""
     import torch
 
     from compactattention_amd import ops
@@ -444,6 +447,13 @@ def paged_pool_line(dev, q, k_new, v_new, kc, vc, P, cap, hkv, rule, splits, tab
         ops.attn_fwd(q, KP, VP, tb, ct, P, scale, cap, hkv, out=out_p, num_splits=splits, workspace=ws)
         return tb, ct
 
+    def run_for(fn, seconds):
+        end = time.perf_counter() + seconds
+        while time.perf_counter() < end:
+            fn()
+            torch.cuda.synchronize()
+
+    run_for(step, settle)
     for _ in range(5):
         step()
     torch.cuda.synchronize()
@@ -461,6 +471,7 @@ def paged_pool_line(dev, q, k_new, v_new, kc, vc, P, cap, hkv, rule, splits, tab
     torch.cuda.synchronize()
     same_out = bool(torch.equal(out_p.view(torch.int16), out_hf.view(torch.int16)))
     attn = lambda: ops.attn_fwd(q, KP, VP, tb, ct, P, scale, cap, hkv, out=out_p, num_splits=splits, workspace=ws)
+    run_for(attn, settle)
     attn_us = timed(attn)
     line = {
         "workload": "config 2 with K/V in a global page pool [pages, 64, 128] read through a page table whose "
