@@ -886,15 +886,19 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
     //    requests of one length, two (512) for ragged batches, at least ~16 blocks per
     //    split, at most 16 splits;
     //  - dense decode with <= 16 rows (attn_decode_kernel): one round (256 slots), at least
-    //    ~32 blocks per split (4 per wave), at most 64 splits.  Its eight waves stream
-    //    blocks on their own, so one long item per CU beats two shorter ones.
+    //    4 blocks per split, at most 32 splits.  Its eight waves stream blocks on their own,
+    //    so one long item per CU beats two shorter ones (64 splits of a 128K-token cache,
+    //    two rounds: 107.6 vs 99.6 us for 32), while a short cache gains from more CUs even
+    //    when some waves of each item idle (32 Q / 8 KV heads: 4K tokens 26.3 -> 11.1 us,
+    //    16K 30.3 -> 21.1 us, four 4K requests 30.0 -> 19.5 us against a floor of 32 blocks
+    //    per split; 4 blocks per split at 1K tokens: 9.9 us, 9.0 and 9.5 us for 8 and 16 splits).
     //  - dense decode with more rows runs attn_fwd_kernel with the prefill sizing and up to
     //    64 splits.
     const bool dec = attn_uses_decode_kernel(s, dense);
     plan->may_unsplit = 0;
     const int slots = dec ? 256 : 512;
-    const int min_blocks = dec ? 32 : 16;
-    const int max_splits = dense ? kMaxDecodeSplits : kMaxPrefillSplits;
+    const int min_blocks = dec ? 4 : 16;
+    const int max_splits = dec ? 32 : dense ? kMaxDecodeSplits : kMaxPrefillSplits;
     const int rows_total = s.Lq * s.G;
     const int ntiles = dec ? 1 : (rows_total + kBM - 1) / kBM;
     double total = 0.0;

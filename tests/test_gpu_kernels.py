@@ -760,8 +760,8 @@ def test_decode_groups_and_query_rows(gpu, G, Lq):
 
 
 def test_decode_long_context_plan(gpu):
-    """A 32K-token request beside a short one: the plan splits the long rows (at least 16
-    blocks per split), so the result goes through the LSE merge."""
+    """A 32K-token request beside a short one: the plan splits the long rows (at least 4
+    blocks per split, at most 32 splits), so the result goes through the LSE merge."""
     _print_case(test="decode_long")
     kv = [64 * 512 + 1, 5000]
     cap = (max(kv) + 63) // 64
