@@ -913,17 +913,20 @@ void attn_plan(const Shape& s, const int32_t* nkb, int forced, bool dense, Split
         // each request's blocks measured slower on ragged batches (config 4: 380 vs 319 us
         // sparse, 2386 vs 2077 us dense), and the blocks a request selects are device data
         // the host does not see.
-        //  - Requests of one length: about one round of work items (one per CU).  Their rows'
-        //    lists have near-equal lengths, so the items stay balanced, and fewer splits
-        //    write fewer partials for the merge (config 2, 128 row tiles: 2 splits 513 us,
-        //    4 splits 522 us, 8 splits 549 us).  Row tiles that fill three quarters of the
-        //    CUs run unsplit (config-3 chunks, 256 tiles: no partials or merge).
+        //  - Requests of one length: at most one round of work items (one per CU).  Their
+        //    rows' lists have near-equal lengths, so the items stay balanced, and fewer
+        //    splits write fewer partials for the merge (config 2, 128 row tiles: 2 splits
+        //    513 us, 4 splits 522 us, 8 splits 549 us).  The count rounds down: a partial
+        //    second round costs a whole item's time (28 Q / 4 KV heads, 16K tokens, chunk
+        //    512, 56 row tiles: 5 splits, 280 items, 195 us against 134 us for 4).  Row
+        //    tiles that fill three quarters of the CUs run unsplit (config-3 chunks, 256
+        //    tiles: no partials or merge).
         //  - Ragged batches: about two rounds, which balances their long rows against the
         //    short ones.
         bool same_len = true;
         for (int b = 1; b < s.B; ++b) same_len = same_len && nkb[b] == nkb[0];
         const int units = s.B * s.Hkv * ntiles;
-        forced = static_cast<int>((same_len ? 256 : slots) / (double)units + 0.5);
+        forced = same_len ? 256 / units : static_cast<int>(slots / (double)units + 0.5);
         forced = min(forced, max(1, nkb_max / min_blocks));
         forced = max(1, min(forced, max_splits));
         if (same_len && units * 4 >= 3 * 256) forced = 1;
