@@ -694,13 +694,15 @@ def ragged_batch(dev, pasts=(16384, 49152, 98304, 131072), chunk=512, hq=28, hkv
 def decode_lines(dev, hq=32, hkv=8):
     """Dense decode (one new token per request over its whole cache) with Llama-3.1-8B heads:
     one attention launch (+ split merge) per layer.  HBM-bound: every cached K/V byte is read
-    once, so the figure of merit is cached bytes / launch time against 8 TB/s."""
+    once, so the figure of merit is cached bytes / launch time against 8 TB/s.  Each line has
+    its eager per-call time (events) and its device time from HIP-graph replays: a short
+    cache's call takes less device time than the host needs to launch it."""
     import torch
 
     from compactattention_amd import ops
 
     lines = []
-    for kv_len in ([131072], [32768] * 8, [4096, 16384, 65536, 131072]):
+    for kv_len in ([131072], [32768] * 8, [4096, 16384, 65536, 131072], [4096] * 4):
         B = len(kv_len)
         cap = (max(kv_len) + 63) // 64
         g = torch.Generator(device=dev).manual_seed(5)
@@ -724,8 +726,27 @@ def decode_lines(dev, hq=32, hkv=8):
         b_.record()
         torch.cuda.synchronize()
         us = a.elapsed_time(b_) / n * 1e3
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fn()
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(10):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(5):
+            graph.replay()
+        b_.record()
+        torch.cuda.synchronize()
+        us_graph = a.elapsed_time(b_) / 50 * 1e3
+        del graph
         kv_bytes = sum(kv_len) * hkv * 128 * 2 * 2
-        lines.append({"kv_len": kv_len, "us_per_layer": round(us, 1),
+        lines.append({"kv_len": kv_len, "us_per_layer": round(us, 1), "us_per_layer_graph": round(us_graph, 1),
                       "hbm_gbps": round(kv_bytes / (us * 1e-6) / 1e9, 1),
                       "hbm_frac": round(kv_bytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4)})
         del k, v, q, K, V, out, ws
