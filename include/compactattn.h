@@ -327,7 +327,7 @@ int ca_dense_table(const ca_dims* dims, const int32_t* past_blocks_host, int32_t
  * the trailing run of blocks that reach past the tile's first query, so an out-of-order
  * row could let a query see later keys.
  * num_splits >= 1 splits every row's block list that many ways; num_splits = 0 picks one
- * count for the launch (ca_attn_pick_splits) with at least ~16 blocks per split: about 256
+ * count for the launch (ca_attn_pick_splits) with at least ~16 blocks per split: at most 256
  * work items (row tiles x splits, one per CU) when all requests have one length, 1 when
  * their row tiles alone fill three quarters of the 256 CUs, and about 512 for ragged
  * batches (a ragged launch whose row tiles fill three quarters of the CUs runs unsplit when
@@ -379,8 +379,9 @@ int32_t ca_attn_pick_splits(const ca_dims* dims, const int32_t* past_blocks_host
  * kv_len_host[b] tokens: row t attends to keys j <= kv_len - q_len + t, read through the
  * K/V layouts (blocks 0 .. ceil(kv_len/64)-1, page table if given; kv_len need not be a
  * multiple of 64).  q/out [B, q_len, Hq, 128], lse as ca_attn_fwd.  The block lists are
- * split KV-wise (num_splits 1..64, or 0 for a per-request plan) and merged by LSE; more
- * than one split needs ca_attn_decode_workspace_size() bytes of workspace.
+ * split KV-wise (num_splits 1..64, or 0 for a per-request plan: about 256 work items, at
+ * least 4 blocks per split, at most 32 splits) and merged by LSE; more than one split needs
+ * ca_attn_decode_workspace_size() bytes of workspace.
  * Replaces: the q_len == 1 branch of LlamaSeerAttentionChunkedDense.forward
  * (compact_attn/prefill_sparse/llama/modeling_llama_seerattn_chunked_dense.py:878-894), i.e.
  * _dense_prefill_full_kv / flash_attn_with_kvcache over the updated cache.
