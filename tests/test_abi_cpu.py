@@ -97,6 +97,43 @@ def test_layout_and_workspace_validation():
     assert lib.ca_attn_pick_splits(ctypes.byref(d), _past(0)) >= 1
 
 
+@pytest.mark.parametrize("B,lq,hq,hkv,past,expect", [
+    (1, 1024, 32, 8, 2048, 2),  # config 2: 128 row tiles, one round of 256 work items
+    (1, 256, 32, 8, 128, 8),    # config 0: 32 row tiles (also the 16-blocks-per-split floor)
+    (1, 2048, 32, 8, 1024, 1),  # a config-3 chunk: 256 row tiles fill the CUs unsplit
+    (1, 512, 28, 4, 256, 4),    # 56 row tiles: 4 splits (224 items), not 5 (280: two rounds)
+    (1, 1024, 24, 6, 2048, 2),  # 96 row tiles: 2 splits (192 items), not 3 (288)
+])
+def test_prefill_automatic_split_count(B, lq, hq, hkv, past, expect):
+    """Requests of one length get the largest split count whose work items fit one round of
+    the 256 CUs (none when the row tiles alone fill three quarters of them)."""
+    d = _dims(batch=B, q_len=lq, num_q_heads=hq, num_kv_heads=hkv, kv_cap=past + lq // 64)
+    n = _hip.lib().ca_attn_pick_splits(ctypes.byref(d), _past(*([past] * B)))
+    assert n == expect
+    units = B * hkv * -(-lq * (hq // hkv) // 256)
+    assert n == 1 or n * units <= 256
+
+
+@pytest.mark.parametrize("kv,expect", [
+    ([1024], 4),       # 16 blocks: the floor of 4 blocks per split
+    ([4096], 16),      # 64 blocks: 4 per split, 128 work items
+    ([16384], 32),     # 256 blocks: the cap of 32 splits, 256 work items
+    ([131072], 32),    # 2048 blocks: 64 per split, 256 work items
+    ([4096] * 4, 8),   # 32 KV rows x 8 splits = 256 work items
+    ([64], 1),         # one block: no split, no workspace
+])
+def test_decode_automatic_split_count(kv, expect):
+    """Decode's per-request plan (32 Q / 8 KV heads, one token): about 256 work items, at least
+    4 blocks per split, at most 32 splits; read back from the workspace size it asks for."""
+    B, hq, hkv = len(kv), 32, 8
+    d = _dims(batch=B, q_len=1, num_q_heads=hq, num_kv_heads=hkv, kv_cap=(max(kv) + 63) // 64)
+    need = _hip.lib().ca_attn_decode_workspace_size(ctypes.byref(d), _past(*kv), 0)
+    rows = B * hkv * (hq // hkv)
+    splits = 1 if need == 0 else (need - 16) // (rows * 129 * 4)
+    assert need == 0 or need == splits * rows * 129 * 4 + 16
+    assert splits == expect
+
+
 @pytest.mark.parametrize("dims,kv_len,code,msg", [
     (_dims(batch=0), (1,), _hip.CA_ERR_INVALID, "batch"),
     (_dims(q_len=0), (1,), _hip.CA_ERR_INVALID, "q_len"),
