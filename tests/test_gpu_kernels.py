@@ -705,6 +705,26 @@ def test_attention_all_selected_equals_dense(gpu):
 
 
 # ----------------------------------------------------------------------------- decode
+def test_attention_max_batch(gpu):
+    """CA_MAX_BATCH (64) requests of ragged lengths (0-16 past blocks) in one launch, 2 KV
+    heads each (128 KV rows), under the automatic plan, against the fp64 oracle."""
+    _print_case(test="attention_max_batch")
+    g = torch.Generator().manual_seed(95)
+    past = [64 * int(x) for x in torch.randint(0, 17, (64,), generator=g)]
+    _attn_case(gpu, past, 64, 4, 2, "heads_first", 0, 0.4, seed=95)
+
+
+def test_attention_more_kv_rows_than_the_placement_table(gpu):
+    """36 requests x 16 KV heads = 576 KV rows, more than the 512 placement units the plan
+    holds: work items are decoded by request offsets instead of per-XCD units (automatic
+    plan and a forced split count), against the fp64 oracle."""
+    g = torch.Generator().manual_seed(96)
+    past = [64 * int(x) for x in torch.randint(0, 17, (36,), generator=g)]
+    for splits in (0, 2):
+        _print_case(test="attention_576_rows", splits=splits)
+        _attn_case(gpu, past, 64, 16, 16, "heads_first", splits, 0.4, seed=96)
+
+
 def _decode_case(gpu, kv_len, Lq, Hq, Hkv, layout, splits, seed, with_prefill_check=False):
     """Dense decode over each request's whole cache against the fp64 oracle.  Cache slots
     past kv_len hold NaN: the kernel must neither read them into the result nor let them
@@ -757,6 +777,17 @@ def test_decode_layouts_and_splits(gpu, layout, splits):
 def test_decode_groups_and_query_rows(gpu, G, Lq):
     _print_case(test="decode_groups", G=G, Lq=Lq)
     _decode_case(gpu, [Lq, 64 * 9 + 7, 1000], Lq, 2 * G, 2, "heads_first", 0, seed=60 + G)
+
+
+def test_decode_max_batch_many_rows(gpu):
+    """CA_MAX_BATCH (64) requests x 16 KV heads = 1024 KV rows (more than the plan's 512
+    placement units), ragged unaligned lengths, automatic and forced splits, against the
+    fp64 decode oracle."""
+    g = torch.Generator().manual_seed(97)
+    kv = [int(x) for x in torch.randint(1, 1000, (64,), generator=g)]
+    for splits in (0, 3):
+        _print_case(test="decode_1024_rows", splits=splits)
+        _decode_case(gpu, kv, 1, 16, 16, "heads_first", splits, seed=97)
 
 
 def test_decode_long_context_plan(gpu):
